@@ -1,0 +1,168 @@
+// C ABI of libdraco_gguf.so: argument validation, error reporting and
+// dispatch to the HIP kernels.  Declarations: include/draco_gguf.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "draco_internal.h"
+#include "gguf_common.h"
+
+namespace draco {
+
+static thread_local char g_last_error[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(DRACO_EHIP, "%s launch failed: %s", what, hipGetErrorString(e));
+  return DRACO_OK;
+}
+
+namespace {
+
+struct TypeInfo {
+  int base;
+  bool d_last;
+  int qk;
+  int bytes;
+};
+
+int decode_type(int ggml_type, TypeInfo* t) {
+  const int base = ggml_type & ~DRACO_GGUF_Q6K_D_LAST;
+  const bool d_last = (ggml_type & DRACO_GGUF_Q6K_D_LAST) != 0;
+  switch (base) {
+    case kQ8_0: *t = {base, false, 32, 34}; break;
+    case kQ4_0: *t = {base, false, 32, 18}; break;
+    case kQ4_K: *t = {base, false, 256, 144}; break;
+    case kQ6_K: *t = {base, d_last, 256, 210}; break;
+    default:
+      return set_error(DRACO_EINVAL_QTYPE,
+                       "GGUF quantization type %d is not supported by this build (supported: Q8_0=8, Q4_0=2, "
+                       "Q4_K=12, Q6_K=14)",
+                       ggml_type);
+  }
+  if (d_last && base != kQ6_K)
+    return set_error(DRACO_EINVAL_QTYPE, "layout flag DRACO_GGUF_Q6K_D_LAST only applies to Q6_K (got type %d)",
+                     ggml_type);
+  return DRACO_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Dimension limits: row and unit indices are 32-bit inside the kernels.
+constexpr int64_t kMaxDim = (int64_t)1 << 30;
+
+int check_matrix(const TypeInfo& t, int64_t n, int64_t k) {
+  if (n <= 0 || k <= 0 || n > kMaxDim || k > kMaxDim)
+    return set_error(DRACO_EINVAL_SHAPE, "invalid weight shape [%lld, %lld]", (long long)n, (long long)k);
+  if (k % t.qk != 0)
+    return set_error(DRACO_EINVAL_SHAPE, "GGUF row length %lld is not divisible by block size %d for ggml type %d",
+                     (long long)k, t.qk, t.base);
+  return DRACO_OK;
+}
+
+int check_bytes(const TypeInfo& t, int64_t n, int64_t k, size_t have, const char* name) {
+  const int64_t need = n * (k / t.qk) * t.bytes;
+  if ((uint64_t)need > (uint64_t)have)
+    return set_error(DRACO_EINVAL_SHAPE, "%s holds %zu bytes but a [%lld, %lld] ggml type %d tensor needs %lld",
+                     name, have, (long long)n, (long long)k, t.base, (long long)need);
+  return DRACO_OK;
+}
+
+int check_ptr(const void* p, const char* name) {
+  if (p == nullptr) return set_error(DRACO_EINVAL_ARG, "%s is NULL", name);
+  if (!aligned16(p)) return set_error(DRACO_EINVAL_ARG, "%s is not 16-byte aligned", name);
+  return DRACO_OK;
+}
+
+}  // namespace
+}  // namespace draco
+
+using namespace draco;
+
+extern "C" {
+
+int draco_gguf_abi_version(void) { return 1; }
+
+const char* draco_gguf_last_error(void) { return g_last_error; }
+
+int draco_gguf_block_info(int ggml_type, int* qk, int* block_bytes) {
+  TypeInfo t;
+  if (int rc = decode_type(ggml_type, &t)) return rc;
+  if (qk) *qk = t.qk;
+  if (block_bytes) *block_bytes = t.bytes;
+  return DRACO_OK;
+}
+
+int draco_gguf_dequant_f32(int ggml_type, const void* blocks, size_t blocks_bytes, float* out, int64_t n_rows,
+                           int64_t k, void* stream) {
+  g_last_error[0] = 0;
+  TypeInfo t;
+  if (int rc = decode_type(ggml_type, &t)) return rc;
+  if (int rc = check_matrix(t, n_rows, k)) return rc;
+  if (int rc = check_bytes(t, n_rows, k, blocks_bytes, "blocks")) return rc;
+  if (int rc = check_ptr(blocks, "blocks")) return rc;
+  if (int rc = check_ptr(out, "out")) return rc;
+  return dequant_dispatch(t.base, t.d_last, blocks, out, n_rows, k, static_cast<hipStream_t>(stream));
+}
+
+int draco_gguf_gemv(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype, const float* bias,
+                    float* y, int64_t m, int64_t n, int64_t k, void* stream) {
+  g_last_error[0] = 0;
+  TypeInfo t;
+  if (int rc = decode_type(ggml_type, &t)) return rc;
+  if (int rc = check_matrix(t, n, k)) return rc;
+  if (int rc = check_bytes(t, n, k, w_bytes, "w")) return rc;
+  if (m < 1 || m > 16)
+    return set_error(DRACO_EINVAL_SHAPE, "GEMV takes 1..16 activation rows, got %lld", (long long)m);
+  if (x_dtype != DRACO_DTYPE_F32 && x_dtype != DRACO_DTYPE_BF16)
+    return set_error(DRACO_EINVAL_ARG, "unknown activation dtype %d", x_dtype);
+  if (int rc = check_ptr(w, "w")) return rc;
+  if (int rc = check_ptr(x, "x")) return rc;
+  if (int rc = check_ptr(y, "y")) return rc;
+  return gemv_dispatch(t.base, t.d_last, w, x, x_dtype == DRACO_DTYPE_BF16, bias, y, (int)m, (int)n, (int)k,
+                       static_cast<hipStream_t>(stream));
+}
+
+int draco_gguf_gemm(int ggml_type, const void* w, size_t w_bytes, const void* x_bf16, const float* bias, float* y,
+                    int64_t m, int64_t n, int64_t k, void* stream) {
+  g_last_error[0] = 0;
+  TypeInfo t;
+  if (int rc = decode_type(ggml_type, &t)) return rc;
+  if (int rc = check_matrix(t, n, k)) return rc;
+  if (int rc = check_bytes(t, n, k, w_bytes, "w")) return rc;
+  if (m < 1 || m > kMaxDim) return set_error(DRACO_EINVAL_SHAPE, "invalid token count %lld", (long long)m);
+  if (int rc = check_ptr(w, "w")) return rc;
+  if (int rc = check_ptr(x_bf16, "x")) return rc;
+  if (int rc = check_ptr(y, "y")) return rc;
+  return gemm_dispatch(t.base, t.d_last, w, x_bf16, bias, y, (int)m, (int)n, (int)k,
+                       static_cast<hipStream_t>(stream));
+}
+
+int draco_gguf_linear(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype, const float* bias,
+                      float* y, int64_t m, int64_t n, int64_t k, void* stream) {
+  if (m >= 1 && m <= 16) return draco_gguf_gemv(ggml_type, w, w_bytes, x, x_dtype, bias, y, m, n, k, stream);
+  if (x_dtype == DRACO_DTYPE_BF16) return draco_gguf_gemm(ggml_type, w, w_bytes, x, bias, y, m, n, k, stream);
+  g_last_error[0] = 0;
+  if (m < 1 || m > kMaxDim) return set_error(DRACO_EINVAL_SHAPE, "invalid token count %lld", (long long)m);
+  if (x_dtype != DRACO_DTYPE_F32) return set_error(DRACO_EINVAL_ARG, "unknown activation dtype %d", x_dtype);
+  // float32 activations, many rows: 16-row GEMV tiles.  Tile row offsets keep x 16-byte aligned
+  // (k is a multiple of 32); y needs n % 4 == 0.
+  if (n % 4 != 0) return set_error(DRACO_EINVAL_SHAPE, "float32 activations with m > 16 need n divisible by 4");
+  for (int64_t m0 = 0; m0 < m; m0 += 16) {
+    const int64_t mt = m - m0 < 16 ? m - m0 : 16;
+    const float* xt = static_cast<const float*>(x) + m0 * k;
+    int rc = draco_gguf_gemv(ggml_type, w, w_bytes, xt, x_dtype, bias, y + m0 * n, mt, n, k, stream);
+    if (rc) return rc;
+  }
+  return DRACO_OK;
+}
+
+}  // extern "C"

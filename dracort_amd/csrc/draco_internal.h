@@ -1,0 +1,27 @@
+// Internal helpers shared by the HIP translation units of libdraco_gguf.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/draco_gguf.h"
+
+namespace draco {
+
+// Records a formatted message in the calling thread's last-error slot and
+// returns `code` (one of the DRACO_E* values).
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// hipGetLastError() after a launch -> DRACO_OK or DRACO_EHIP with the HIP message.
+int check_launch(const char* what);
+
+int dequant_dispatch(int qtype, bool d_last, const void* w, float* out, int64_t n_rows, int64_t k,
+                     hipStream_t s);
+
+int gemv_dispatch(int qtype, bool d_last, const void* w, const void* x, bool x_bf16, const float* bias,
+                  float* y, int m, int n, int k, hipStream_t s);
+
+int gemm_dispatch(int qtype, bool d_last, const void* w, const void* x_bf16, const float* bias, float* y,
+                  int m, int n, int k, hipStream_t s);
+
+}  // namespace draco

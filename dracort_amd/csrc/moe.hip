@@ -1,0 +1,310 @@
+// Sparse MoE FFN over GGUF-quantized experts on gfx950.
+//
+// Replaces TopKRouter.forward (draco/models/moe/router.py:81-120) and
+// ExpertGroup.forward / Expert.forward (draco/models/moe/expert.py:47-49,
+// 77-116) with four launches and no host synchronization:
+//
+//  1. moe_route_kernel (one workgroup): per token, top-k of the router logits
+//     (ties -> lower expert index), softmax over the k logits, renormalised by
+//     their sum (router.py:106-111); slots sorted by expert id.  Tokens are
+//     then grouped by expert: counts, exclusive offsets, and for every expert
+//     its tokens in ascending order (a block-wide ballot/popcount scan, so
+//     the grouping is deterministic).
+//  2. moe_up_kernel: grid (row blocks of the intermediate dim, experts).  Each
+//     wave runs the register GEMV core on W_gate[e] and W_up[e] for the
+//     expert's gathered tokens (16 at a time) and writes
+//     h = silu(gate) * up in float32.
+//  3. moe_down_kernel: the same core on W_down[e] over h, one output row per
+//     (expert, token) assignment.
+//  4. moe_combine_kernel: y[t] = sum over the token's slots in ascending
+//     expert order of weight * down_out, the reference's index_add_ order.
+#include "draco_internal.h"
+#include "gemv_core.h"
+
+namespace draco {
+
+constexpr int kMaxExperts = 64;
+constexpr int kMaxTopK = 8;
+constexpr int kMoeMT = 16;
+
+struct ExpertPtrs {
+  const uint8_t* p[kMaxExperts];
+};
+
+struct MoeWs {
+  int* sel_e;       // [T*k] expert of each slot, slots ascending by expert
+  float* sel_w;     // [T*k] routing weight of each slot
+  int* slot_pos;    // [T*k] assignment row of each slot
+  int* assign_tok;  // [T*k] token of each assignment row, grouped by expert
+  int* counts;      // [E]
+  int* offsets;     // [E + 1]
+  float* h;         // [T*k, inter]  silu(gate) * up
+  float* yk;        // [T*k, hidden] expert outputs
+};
+
+static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+static size_t moe_ws_layout(int64_t T, int64_t H, int64_t I, int E, int k, char* base, MoeWs* ws) {
+  const size_t tk = (size_t)T * k;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  MoeWs w;
+  w.sel_e = (int*)take(tk * 4);
+  w.sel_w = (float*)take(tk * 4);
+  w.slot_pos = (int*)take(tk * 4);
+  w.assign_tok = (int*)take(tk * 4);
+  w.counts = (int*)take((size_t)E * 4);
+  w.offsets = (int*)take((size_t)(E + 1) * 4);
+  w.h = (float*)take(tk * (size_t)I * 4);
+  w.yk = (float*)take(tk * (size_t)H * 4);
+  if (ws) *ws = w;
+  return off;
+}
+
+__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int T, int E, int k,
+                                                        MoeWs ws) {
+  __shared__ int cnt[kMaxExperts];
+  __shared__ int offs[kMaxExperts + 1];
+  __shared__ int running[kMaxExperts];
+  __shared__ int wave_tot[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // 1. top-k, softmax, renormalise, sort slots by expert
+  for (int t = tid; t < T; t += 256) {
+    const float* lg = logits + (size_t)t * E;
+    int idx[kMaxTopK];
+    float val[kMaxTopK];
+    uint64_t taken = 0;
+    for (int j = 0; j < k; ++j) {
+      int best = -1;
+      float bv = 0.f;
+      for (int e = 0; e < E; ++e) {
+        if (taken >> e & 1ull) continue;
+        const float v = lg[e];
+        if (best < 0 || v > bv) { best = e; bv = v; }
+      }
+      taken |= 1ull << best;
+      idx[j] = best;
+      val[j] = bv;
+    }
+    float ex[kMaxTopK], s = 0.f;
+    for (int j = 0; j < k; ++j) { ex[j] = __expf(val[j] - val[0]); s += ex[j]; }
+    float s2 = 0.f;
+    for (int j = 0; j < k; ++j) { ex[j] = ex[j] / s; s2 += ex[j]; }
+    for (int j = 0; j < k; ++j) ex[j] = ex[j] / s2;
+    for (int a = 1; a < k; ++a) {  // insertion sort by expert id
+      int ie = idx[a];
+      float we = ex[a];
+      int b = a - 1;
+      while (b >= 0 && idx[b] > ie) { idx[b + 1] = idx[b]; ex[b + 1] = ex[b]; --b; }
+      idx[b + 1] = ie;
+      ex[b + 1] = we;
+    }
+    for (int j = 0; j < k; ++j) {
+      ws.sel_e[t * k + j] = idx[j];
+      ws.sel_w[t * k + j] = ex[j];
+    }
+  }
+  for (int e = tid; e < E; e += 256) { cnt[e] = 0; running[e] = 0; }
+  __syncthreads();
+
+  // 2. per-expert counts and exclusive offsets
+  for (int s = tid; s < T * k; s += 256) atomicAdd(&cnt[ws.sel_e[s]], 1);
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    for (int e = 0; e < E; ++e) { offs[e] = acc; acc += cnt[e]; }
+    offs[E] = acc;
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += 256) { ws.counts[e] = cnt[e]; ws.offsets[e] = offs[e]; }
+  if (tid == 0) ws.offsets[E] = offs[E];
+
+  // 3. deterministic grouping: tokens of expert e in ascending token order
+  for (int cb = 0; cb < T; cb += 256) {
+    const int t = cb + tid;
+    for (int e = 0; e < E; ++e) {
+      int js = -1;
+      if (t < T)
+        for (int j = 0; j < k; ++j)
+          if (ws.sel_e[t * k + j] == e) js = j;
+      const bool flag = js >= 0;
+      const uint64_t mask = __ballot(flag);
+      const int rank = __popcll(mask & ((1ull << lane) - 1ull));
+      if (lane == 0) wave_tot[wave] = __popcll(mask);
+      __syncthreads();
+      int before = 0, total = 0;
+      for (int w = 0; w < 4; ++w) {
+        if (w < wave) before += wave_tot[w];
+        total += wave_tot[w];
+      }
+      if (flag) {
+        const int pos = offs[e] + running[e] + before + rank;
+        ws.assign_tok[pos] = t;
+        ws.slot_pos[t * k + js] = pos;
+      }
+      __syncthreads();
+      if (tid == 0) running[e] += total;
+      __syncthreads();
+    }
+  }
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.f + __expf(-g)); }
+
+template <int QT, bool XBF16, int R>
+__global__ __launch_bounds__(256) void moe_up_kernel(ExpertPtrs wg, ExpertPtrs wu, const void* __restrict__ x,
+                                                     int H, int I, MoeWs ws) {
+  const int e = blockIdx.y;
+  const int cnt = ws.counts[e];
+  if (cnt == 0) return;
+  const int off = ws.offsets[e];
+  const int lane = threadIdx.x & 63;
+  const int n0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
+  if (n0 >= I) return;
+  const int64_t row_bytes = (int64_t)(H / Fmt<QT>::QK) * Fmt<QT>::BYTES;
+  const size_t xstride = XBF16 ? (size_t)H * 2 : (size_t)H * 4;
+  const uint8_t* xb = static_cast<const uint8_t*>(x);
+  for (int t0 = 0; t0 < cnt; t0 += kMoeMT) {
+    const int mt = min(kMoeMT, cnt - t0);
+    const int* toks = ws.assign_tok + off + t0;
+    auto xrow = [&](int mi) { return (const void*)(xb + (size_t)toks[mi] * xstride); };
+    float ag[R][kMoeMT], au[R][kMoeMT];
+    gemv_accumulate<QT, false, kMoeMT, XBF16, R>(wg.p[e], row_bytes, n0, I, H, mt, xrow, ag);
+    gemv_accumulate<QT, false, kMoeMT, XBF16, R>(wu.p[e], row_bytes, n0, I, H, mt, xrow, au);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int mi = 0; mi < kMoeMT; ++mi) {
+        const float g = wave_sum(ag[r][mi]);
+        const float u = wave_sum(au[r][mi]);
+        if (lane == 0 && mi < mt && n0 + r < I) ws.h[(size_t)(off + t0 + mi) * I + n0 + r] = silu_f(g) * u;
+      }
+  }
+}
+
+template <int QT, int R>
+__global__ __launch_bounds__(256) void moe_down_kernel(ExpertPtrs wd, int H, int I, MoeWs ws) {
+  const int e = blockIdx.y;
+  const int cnt = ws.counts[e];
+  if (cnt == 0) return;
+  const int off = ws.offsets[e];
+  const int lane = threadIdx.x & 63;
+  const int n0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
+  if (n0 >= H) return;
+  const int64_t row_bytes = (int64_t)(I / Fmt<QT>::QK) * Fmt<QT>::BYTES;
+  for (int t0 = 0; t0 < cnt; t0 += kMoeMT) {
+    const int mt = min(kMoeMT, cnt - t0);
+    const float* hb = ws.h + (size_t)(off + t0) * I;
+    auto xrow = [&](int mi) { return (const void*)(hb + (size_t)mi * I); };
+    float acc[R][kMoeMT];
+    gemv_accumulate<QT, false, kMoeMT, false, R>(wd.p[e], row_bytes, n0, H, I, mt, xrow, acc);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int mi = 0; mi < kMoeMT; ++mi) {
+        const float v = wave_sum(acc[r][mi]);
+        if (lane == 0 && mi < mt && n0 + r < H) ws.yk[(size_t)(off + t0 + mi) * H + n0 + r] = v;
+      }
+  }
+}
+
+__global__ __launch_bounds__(256) void moe_combine_kernel(float* __restrict__ y, int H, int k, MoeWs ws) {
+  const int t = blockIdx.y;
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= H) return;
+  float acc = 0.f;
+  for (int j = 0; j < k; ++j) {
+    const int p = ws.slot_pos[t * k + j];
+    const float contrib = ws.yk[(size_t)p * H + n] * ws.sel_w[t * k + j];
+    acc = acc + contrib;
+  }
+  y[(size_t)t * H + n] = acc;
+}
+
+template <int QT>
+static int launch_moe(const ExpertPtrs& wg, const ExpertPtrs& wu, const ExpertPtrs& wd, const float* logits,
+                      const void* x, bool xbf16, float* y, int T, int H, int I, int E, int k, const MoeWs& ws,
+                      hipStream_t s) {
+  constexpr int R = 1;
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), 0, s, logits, T, E, k, ws);
+  if (int rc = check_launch("moe_route")) return rc;
+  const dim3 gup((unsigned)((I + 4 * R - 1) / (4 * R)), (unsigned)E);
+  if (xbf16)
+    hipLaunchKernelGGL((moe_up_kernel<QT, true, R>), gup, dim3(256), 0, s, wg, wu, x, H, I, ws);
+  else
+    hipLaunchKernelGGL((moe_up_kernel<QT, false, R>), gup, dim3(256), 0, s, wg, wu, x, H, I, ws);
+  if (int rc = check_launch("moe_up")) return rc;
+  const dim3 gdown((unsigned)((H + 4 * R - 1) / (4 * R)), (unsigned)E);
+  hipLaunchKernelGGL((moe_down_kernel<QT, R>), gdown, dim3(256), 0, s, wd, H, I, ws);
+  if (int rc = check_launch("moe_down")) return rc;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, s, y, H,
+                     k, ws);
+  return check_launch("moe_combine");
+}
+
+}  // namespace draco
+
+using namespace draco;
+
+extern "C" size_t draco_gguf_moe_workspace_size(int64_t tokens, int64_t hidden, int64_t inter, int n_experts,
+                                                int top_k) {
+  if (tokens < 1 || hidden < 1 || inter < 1 || n_experts < 1 || top_k < 1) return 0;
+  return moe_ws_layout(tokens, hidden, inter, n_experts, top_k, nullptr, nullptr);
+}
+
+extern "C" int draco_gguf_moe_ffn(int ggml_type, const void* const* w_gate, const void* const* w_up,
+                                  const void* const* w_down, size_t expert_w_bytes, const float* router_logits,
+                                  const void* x, int x_dtype, float* y, int64_t tokens, int64_t hidden, int64_t inter,
+                                  int n_experts, int top_k, void* workspace, size_t workspace_bytes, void* stream) {
+  int qk = 0, bb = 0;
+  if (int rc = draco_gguf_block_info(ggml_type, &qk, &bb)) return rc;
+  if (ggml_type & DRACO_GGUF_Q6K_D_LAST)
+    return set_error(DRACO_EINVAL_QTYPE, "MoE experts take reference-layout blocks only");
+  if (n_experts < 1 || n_experts > kMaxExperts)
+    return set_error(DRACO_EINVAL_SHAPE, "n_experts must be in 1..%d, got %d", kMaxExperts, n_experts);
+  if (top_k < 1 || top_k > kMaxTopK || top_k > n_experts)
+    return set_error(DRACO_EINVAL_SHAPE, "top_k must be in 1..min(%d, n_experts), got %d", kMaxTopK, top_k);
+  if (tokens < 1 || tokens * top_k > (1 << 30) || hidden < 1 || inter < 1 || hidden > (1 << 30) ||
+      inter > (1 << 30))
+    return set_error(DRACO_EINVAL_SHAPE, "invalid MoE dims tokens=%lld hidden=%lld inter=%lld",
+                     (long long)tokens, (long long)hidden, (long long)inter);
+  if (hidden % qk || inter % qk)
+    return set_error(DRACO_EINVAL_SHAPE, "hidden (%lld) and inter (%lld) must be multiples of the block size %d",
+                     (long long)hidden, (long long)inter, qk);
+  const uint64_t need_w = (uint64_t)(inter * (hidden / qk)) * (uint64_t)bb;
+  if (expert_w_bytes < need_w)
+    return set_error(DRACO_EINVAL_SHAPE, "expert weights hold %zu bytes, [%lld, %lld] needs %llu", expert_w_bytes,
+                     (long long)inter, (long long)hidden, (unsigned long long)need_w);
+  if (x_dtype != DRACO_DTYPE_F32 && x_dtype != DRACO_DTYPE_BF16)
+    return set_error(DRACO_EINVAL_ARG, "unknown activation dtype %d", x_dtype);
+  if (!w_gate || !w_up || !w_down) return set_error(DRACO_EINVAL_ARG, "expert pointer arrays must not be NULL");
+  auto bad = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) != 0; };
+  if (bad(router_logits) || bad(x) || bad(y) || bad(workspace))
+    return set_error(DRACO_EINVAL_ARG, "router_logits, x, y and workspace must be non-NULL and 16-byte aligned");
+  ExpertPtrs wg{}, wu{}, wd{};
+  for (int e = 0; e < n_experts; ++e) {
+    if (bad(w_gate[e]) || bad(w_up[e]) || bad(w_down[e]))
+      return set_error(DRACO_EINVAL_ARG, "expert %d weight pointer is NULL or misaligned", e);
+    wg.p[e] = static_cast<const uint8_t*>(w_gate[e]);
+    wu.p[e] = static_cast<const uint8_t*>(w_up[e]);
+    wd.p[e] = static_cast<const uint8_t*>(w_down[e]);
+  }
+  MoeWs ws;
+  const size_t need = moe_ws_layout(tokens, hidden, inter, n_experts, top_k, static_cast<char*>(workspace), &ws);
+  if (workspace_bytes < need)
+    return set_error(DRACO_EWORKSPACE, "MoE workspace needs %zu bytes, got %zu", need, workspace_bytes);
+  const bool xbf16 = x_dtype == DRACO_DTYPE_BF16;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int T = (int)tokens, H = (int)hidden, I = (int)inter;
+  switch (ggml_type) {
+    case kQ8_0: return launch_moe<kQ8_0>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+    case kQ4_0: return launch_moe<kQ4_0>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+    case kQ4_K: return launch_moe<kQ4_K>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+    default: return launch_moe<kQ6_K>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+  }
+}

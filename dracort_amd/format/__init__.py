@@ -1,0 +1,14 @@
+"""GGUF block formats handled by the GPU path."""
+
+from dracort_amd.format.gguf import (  # noqa: F401
+    BLOCK_LAYOUTS,
+    GGML_TYPE_Q4_0,
+    GGML_TYPE_Q4_K,
+    GGML_TYPE_Q6_K,
+    GGML_TYPE_Q8_0,
+    Q6K_D_LAST,
+    GgufTensorInfo,
+    layout,
+    row_bytes,
+    tensor_bytes,
+)

@@ -1,0 +1,21 @@
+"""GPU operators of the GGUF quantized-matmul path (HIP kernels, gfx950)."""
+
+from dracort_amd.kernels.gguf import (  # noqa: F401
+    block_layout,
+    gguf_dequantize,
+    gguf_gemm,
+    gguf_gemv,
+    gguf_linear,
+    gguf_moe,
+    moe_workspace_bytes,
+)
+
+__all__ = [
+    "gguf_dequantize",
+    "gguf_linear",
+    "gguf_gemv",
+    "gguf_gemm",
+    "gguf_moe",
+    "moe_workspace_bytes",
+    "block_layout",
+]

@@ -1,0 +1,250 @@
+"""GGUF quantized-matmul operators on MI355X (the ``draco.kernels`` namespace
+counterpart for quantized weights).
+
+Every function takes PyTorch-ROCm tensors, checks shapes, dtypes, devices and
+buffer sizes on the host, and enqueues the HIP kernels of libdraco_gguf.so on
+the current torch stream of the tensors' device.  Nothing here computes on the
+CPU and nothing falls back to another implementation: a missing library or a
+CPU tensor raises.
+
+Reference call sites replaced:
+
+* ``gguf_dequantize``  ``_dequantize`` + ``GGUFReader.get_tensor``
+                       (``draco/format/gguf.py:272-497,820-834``), bit-exact.
+* ``gguf_linear``      ``_linear`` (``draco/runtime/cpu/executor.py:47-79``):
+                       ``activation.astype(f32) @ W.T (+ bias)``
+                       (``draco/runtime/cpu/kernels/generic.py:32-33``) with the
+                       dequantization fused into the GEMV (M <= 16) or GEMM.
+* ``gguf_moe``         ``TopKRouter.forward`` + ``ExpertGroup.forward``
+                       (``draco/models/moe/router.py:81-120``,
+                       ``draco/models/moe/expert.py:77-116``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from dracort_amd import _native
+from dracort_amd.exceptions import DracoFormatError
+from dracort_amd.format.gguf import layout, tensor_bytes
+
+GEMV_MAX_M = 16
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _need_gpu(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on the GPU (got {t.device}); the GGUF path has no CPU implementation")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.data_ptr() % 16 != 0:
+        raise ValueError(f"{name} must be 16-byte aligned")
+
+
+def _same_device(*ts: torch.Tensor) -> None:
+    dev = ts[0].device
+    for t in ts[1:]:
+        if t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+
+
+def _check_weight(qweight: torch.Tensor, ggml_type: int, shape: Tuple[int, int]) -> Tuple[int, int]:
+    _need_gpu(qweight, "qweight")
+    if qweight.dtype != torch.uint8:
+        raise ValueError(f"qweight must be uint8 GGUF block bytes, got {qweight.dtype}")
+    if len(shape) != 2:
+        raise ValueError(f"weight shape must be [N, K], got {shape}")
+    n, k = int(shape[0]), int(shape[1])
+    need = tensor_bytes(ggml_type, (n, k))
+    if qweight.numel() < need:
+        raise DracoFormatError(
+            f"GGUF payload holds {qweight.numel()} bytes but a {shape} ggml type {ggml_type} tensor needs {need}"
+        )
+    return n, k
+
+
+def _x_dtype(x: torch.Tensor) -> int:
+    if x.dtype == torch.float32:
+        return _native.DRACO_DTYPE_F32
+    if x.dtype == torch.bfloat16:
+        return _native.DRACO_DTYPE_BF16
+    raise ValueError(f"activations must be float32 or bfloat16, got {x.dtype}")
+
+
+def gguf_dequantize(
+    qweight: torch.Tensor, ggml_type: int, shape: Tuple[int, int], out: Optional[torch.Tensor] = None
+) -> torch.Tensor:
+    """float32 [N, K] weight, bit-exact to the reference dequantization."""
+    n, k = _check_weight(qweight, ggml_type, shape)
+    if out is None:
+        out = torch.empty((n, k), dtype=torch.float32, device=qweight.device)
+    else:
+        _need_gpu(out, "out")
+        if out.dtype != torch.float32 or out.numel() != n * k:
+            raise ValueError(f"out must be float32 with {n * k} elements")
+    _same_device(qweight, out)
+    lib = _native.load()
+    with torch.cuda.device(qweight.device):
+        rc = lib.draco_gguf_dequant_f32(
+            int(ggml_type), qweight.data_ptr(), qweight.numel(), out.data_ptr(), n, k, _stream(qweight)
+        )
+    _native.check(rc, "gguf_dequantize")
+    return out.view(n, k)
+
+
+def _prep_linear(x, qweight, ggml_type, shape, bias, out):
+    n, k = _check_weight(qweight, ggml_type, shape)
+    _need_gpu(x, "x")
+    if x.shape[-1] != k:
+        raise ValueError(f"x has {x.shape[-1]} features, weight expects K={k}")
+    m = x.numel() // k if x.numel() else 0
+    if m < 1:
+        raise ValueError("x holds no rows")
+    xd = _x_dtype(x)
+    if bias is not None:
+        _need_gpu(bias, "bias")
+        if bias.dtype != torch.float32 or bias.numel() != n:
+            raise ValueError(f"bias must be float32 with {n} elements")
+    out_shape = tuple(x.shape[:-1]) + (n,)
+    if out is None:
+        out = torch.empty(out_shape, dtype=torch.float32, device=x.device)
+    else:
+        _need_gpu(out, "out")
+        if out.dtype != torch.float32 or out.numel() != m * n:
+            raise ValueError(f"out must be float32 with {m * n} elements")
+    _same_device(x, qweight, out, *( [bias] if bias is not None else []))
+    return m, n, k, xd, out
+
+
+def gguf_linear(
+    x: torch.Tensor,
+    qweight: torch.Tensor,
+    ggml_type: int,
+    shape: Tuple[int, int],
+    bias: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """``x @ dequant(W).T (+ bias)`` for x [..., K] (float32 or bfloat16) -> float32 [..., N]."""
+    m, n, k, xd, out = _prep_linear(x, qweight, ggml_type, shape, bias, out)
+    lib = _native.load()
+    with torch.cuda.device(x.device):
+        rc = lib.draco_gguf_linear(
+            int(ggml_type), qweight.data_ptr(), qweight.numel(), x.data_ptr(), xd,
+            bias.data_ptr() if bias is not None else None, out.data_ptr(), m, n, k, _stream(x),
+        )
+    _native.check(rc, "gguf_linear")
+    return out
+
+
+def gguf_gemv(x, qweight, ggml_type, shape, bias=None, out=None) -> torch.Tensor:
+    """Decode GEMV (1..16 activation rows), dequantization fused."""
+    m, n, k, xd, out = _prep_linear(x, qweight, ggml_type, shape, bias, out)
+    if m > GEMV_MAX_M:
+        raise ValueError(f"gguf_gemv takes at most {GEMV_MAX_M} rows, got {m}")
+    lib = _native.load()
+    with torch.cuda.device(x.device):
+        rc = lib.draco_gguf_gemv(
+            int(ggml_type), qweight.data_ptr(), qweight.numel(), x.data_ptr(), xd,
+            bias.data_ptr() if bias is not None else None, out.data_ptr(), m, n, k, _stream(x),
+        )
+    _native.check(rc, "gguf_gemv")
+    return out
+
+
+def gguf_gemm(x, qweight, ggml_type, shape, bias=None, out=None) -> torch.Tensor:
+    """Prefill GEMM (bf16 activations, MFMA), dequantization fused."""
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"gguf_gemm takes bfloat16 activations, got {x.dtype}")
+    m, n, k, xd, out = _prep_linear(x, qweight, ggml_type, shape, bias, out)
+    lib = _native.load()
+    with torch.cuda.device(x.device):
+        rc = lib.draco_gguf_gemm(
+            int(ggml_type), qweight.data_ptr(), qweight.numel(), x.data_ptr(),
+            bias.data_ptr() if bias is not None else None, out.data_ptr(), m, n, k, _stream(x),
+        )
+    _native.check(rc, "gguf_gemm")
+    return out
+
+
+def moe_workspace_bytes(tokens: int, hidden: int, inter: int, n_experts: int, top_k: int) -> int:
+    return int(_native.load().draco_gguf_moe_workspace_size(tokens, hidden, inter, n_experts, top_k))
+
+
+def gguf_moe(
+    x: torch.Tensor,
+    router_logits: torch.Tensor,
+    w_gate: Sequence[torch.Tensor],
+    w_up: Sequence[torch.Tensor],
+    w_down: Sequence[torch.Tensor],
+    ggml_type: int,
+    inter: int,
+    top_k: int = 2,
+    workspace: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Sparse MoE FFN: top-k softmax routing + per-expert GGUF SwiGLU FFN.
+
+    x [T, H] (float32/bfloat16), router_logits [T, E] float32, w_gate[e] /
+    w_up[e] GGUF [inter, H], w_down[e] GGUF [H, inter]; returns float32 [T, H].
+    """
+    _need_gpu(x, "x")
+    _need_gpu(router_logits, "router_logits")
+    if x.dim() != 2:
+        raise ValueError("x must be [tokens, hidden]")
+    t, h = x.shape
+    e = len(w_gate)
+    if not (len(w_up) == e and len(w_down) == e and e >= 1):
+        raise ValueError("w_gate, w_up and w_down must list the same experts")
+    if router_logits.dtype != torch.float32 or tuple(router_logits.shape) != (t, e):
+        raise ValueError(f"router_logits must be float32 [{t}, {e}]")
+    xd = _x_dtype(x)
+    need = tensor_bytes(ggml_type, (inter, h))
+    if tensor_bytes(ggml_type, (h, inter)) != need:
+        raise DracoFormatError("gate/up and down expert shapes disagree")
+    for name, ws in (("w_gate", w_gate), ("w_up", w_up), ("w_down", w_down)):
+        for i, w in enumerate(ws):
+            _need_gpu(w, f"{name}[{i}]")
+            if w.dtype != torch.uint8 or w.numel() < need:
+                raise DracoFormatError(f"{name}[{i}] must be uint8 GGUF blocks of >= {need} bytes")
+            _same_device(x, w)
+    ws_bytes = moe_workspace_bytes(t, h, inter, e, top_k)
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    else:
+        _need_gpu(workspace, "workspace")
+    if out is None:
+        out = torch.empty((t, h), dtype=torch.float32, device=x.device)
+    else:
+        _need_gpu(out, "out")
+        if out.dtype != torch.float32 or out.numel() != t * h:
+            raise ValueError(f"out must be float32 with {t * h} elements")
+    _same_device(x, router_logits, workspace, out)
+    arr = ctypes.c_void_p * e
+    pg = arr(*[w.data_ptr() for w in w_gate])
+    pu = arr(*[w.data_ptr() for w in w_up])
+    pd = arr(*[w.data_ptr() for w in w_down])
+    lib = _native.load()
+    with torch.cuda.device(x.device):
+        rc = lib.draco_gguf_moe_ffn(
+            int(ggml_type), pg, pu, pd, need, router_logits.data_ptr(), x.data_ptr(), xd, out.data_ptr(),
+            t, h, int(inter), e, int(top_k), workspace.data_ptr(), workspace.numel(), _stream(x),
+        )
+    _native.check(rc, "gguf_moe")
+    return out
+
+
+def block_layout(ggml_type: int) -> Tuple[int, int]:
+    """(elements, bytes) per block, from the library (checks it loads)."""
+    host = layout(ggml_type)
+    dev = _native.block_info(ggml_type)
+    if host != dev:
+        raise DracoFormatError(f"block layout mismatch for type {ggml_type}: {host} vs library {dev}")
+    return dev

@@ -1,0 +1,133 @@
+/*
+ * draco_gguf.h -- C ABI of libdraco_gguf.so, the MI355X (gfx950) GGUF
+ * quantized-matmul library.
+ *
+ * Plain C types only: device pointers are `const void*` / `float*` into HBM
+ * (e.g. torch tensor data_ptr()), sizes are int64_t, the stream is a
+ * hipStream_t passed as `void*` (NULL = the null stream).
+ *
+ * Conventions (all entry points):
+ *  - Caller-allocated buffers; the library never allocates or frees caller
+ *    memory.  Pointers are borrowed for the duration of the enqueued work.
+ *  - Every call only ENQUEUES work on `stream` and returns; nothing here
+ *    synchronizes the device.
+ *  - Return 0 on success or a negative DRACO_E* code; the calling thread's
+ *    draco_gguf_last_error() then holds a message.
+ *  - Weight buffers hold GGUF blocks in their native packed layout: an [N, K]
+ *    weight is N rows of K/QK blocks, rows contiguous, blocks along K
+ *    (reference: draco/format/gguf.py:630-648).  Weight, activation and output
+ *    pointers must be 16-byte aligned.  Weight entry points also take the
+ *    byte size of the weight buffer; a buffer shorter than the shape needs
+ *    (a truncated payload) is rejected with DRACO_EINVAL_SHAPE before any
+ *    launch.
+ *  - ggml_type is the GGUF type id, optionally OR-ed with
+ *    DRACO_GGUF_Q6K_D_LAST for Q6_K blocks stored in upstream ggml field order
+ *    (ql, qh, scales, d) instead of the reference's (d, ql, qh, scales).
+ */
+#ifndef DRACO_GGUF_H
+#define DRACO_GGUF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGUF type ids handled here (reference: draco/format/gguf.py:57-72). */
+#define DRACO_GGML_TYPE_Q4_0 2
+#define DRACO_GGML_TYPE_Q8_0 8
+#define DRACO_GGML_TYPE_Q4_K 12
+#define DRACO_GGML_TYPE_Q6_K 14
+/* Layout flag: Q6_K field order of upstream ggml (d stored last). */
+#define DRACO_GGUF_Q6K_D_LAST 0x100
+
+/* Activation dtypes. */
+#define DRACO_DTYPE_F32 0
+#define DRACO_DTYPE_BF16 1
+
+/* Return codes. */
+#define DRACO_OK 0
+#define DRACO_EINVAL_QTYPE (-1) /* unsupported ggml type               */
+#define DRACO_EINVAL_SHAPE (-2) /* K % QK != 0, non-positive or too-large dims, M out of range */
+#define DRACO_EINVAL_ARG (-3)   /* null / misaligned pointer, bad dtype */
+#define DRACO_EHIP (-4)         /* HIP launch or runtime error          */
+#define DRACO_EWORKSPACE (-5)   /* workspace missing or too small       */
+
+/* ABI version of this header (bumped on any signature change). */
+int draco_gguf_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* draco_gguf_last_error(void);
+
+/*
+ * Block geometry of a ggml type: elements per block and bytes per block.
+ * Replaces the lookup in _BLOCK_LAYOUTS (draco/format/gguf.py:75-87).
+ */
+int draco_gguf_block_info(int ggml_type, int* qk, int* block_bytes);
+
+/*
+ * out[n_rows, k] (float32) = dequantize(blocks), bit-exact to the reference
+ * float32 dequant.  Replaces _dequantize(qtype, payload, n)
+ * (draco/format/gguf.py:272-497) as called by GGUFReader.get_tensor
+ * (draco/format/gguf.py:820-834).
+ */
+int draco_gguf_dequant_f32(int ggml_type, const void* blocks, size_t blocks_bytes, float* out, int64_t n_rows,
+                           int64_t k, void* stream);
+
+/*
+ * Decode GEMV with the dequantization fused in:
+ *   y[m, n] = x[m, k] . W[n, k]^T (+ bias[n]),  1 <= m <= 16.
+ * x is float32 or bfloat16 (x_dtype), y and bias (nullable) float32;
+ * accumulation is float32.  Replaces _dequantize followed by
+ * GenericGemmKernel.matmul_f32 (draco/runtime/cpu/kernels/generic.py:32-33)
+ * inside _linear (draco/runtime/cpu/executor.py:47-79), and
+ * QuantizationBackend.quantized_linear (draco/quantization/base.py:86-99).
+ */
+int draco_gguf_gemv(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype, const float* bias,
+                    float* y, int64_t m, int64_t n, int64_t k, void* stream);
+
+/*
+ * Prefill GEMM with the dequantization fused in (weight tiles decoded into
+ * LDS, bf16 MFMA, float32 accumulate and output):
+ *   y[m, n] = x_bf16[m, k] . W[n, k]^T (+ bias[n]),  m >= 1.
+ * Same reference call sites as draco_gguf_gemv, for prompt-sized M.
+ */
+int draco_gguf_gemm(int ggml_type, const void* w, size_t w_bytes, const void* x_bf16, const float* bias, float* y,
+                    int64_t m, int64_t n, int64_t k, void* stream);
+
+/*
+ * _linear for any M: draco_gguf_gemv for m <= 16, draco_gguf_gemm for larger
+ * m with bf16 activations, and 16-row GEMV tiles for larger m with float32
+ * activations.  Replaces _linear (draco/runtime/cpu/executor.py:47-79).
+ */
+int draco_gguf_linear(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype, const float* bias,
+                      float* y, int64_t m, int64_t n, int64_t k, void* stream);
+
+/*
+ * Workspace bytes draco_gguf_moe_ffn needs for `tokens` tokens.
+ */
+size_t draco_gguf_moe_workspace_size(int64_t tokens, int64_t hidden, int64_t inter, int n_experts, int top_k);
+
+/*
+ * Sparse MoE FFN over GGUF experts:
+ *   (idx, w) = top_k(router_logits[t, :]); w = softmax(w); w /= sum(w)
+ *   y[t] = sum over the token's experts e, in ascending e, of
+ *          w_e * W_down[e] . (silu(W_gate[e] . x[t]) * (W_up[e] . x[t]))
+ * w_gate / w_up ([inter, hidden]) and w_down ([hidden, inter]) are HOST arrays
+ * of n_experts device pointers, each buffer at least expert_w_bytes long; x is [tokens, hidden] bfloat16 or float32,
+ * router_logits [tokens, n_experts] float32, y [tokens, hidden] float32.
+ * Routing and grouping run on the device (no host synchronization).
+ * Replaces TopKRouter.forward (draco/models/moe/router.py:81-120) and
+ * ExpertGroup.forward (draco/models/moe/expert.py:77-116).
+ */
+int draco_gguf_moe_ffn(int ggml_type, const void* const* w_gate, const void* const* w_up,
+                       const void* const* w_down, size_t expert_w_bytes, const float* router_logits, const void* x, int x_dtype,
+                       float* y, int64_t tokens, int64_t hidden, int64_t inter, int n_experts, int top_k,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DRACO_GGUF_H */

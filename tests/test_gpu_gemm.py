@@ -1,0 +1,50 @@
+"""GPU parity: prefill GEMM (weight tiles decoded into LDS, bf16 MFMA, fp32
+accumulate) against the oracle's fp64 dequant-then-matmul, <= 1e-3."""
+
+import numpy as np
+import pytest
+import torch
+
+from dracort_amd.kernels import gguf_gemm, gguf_linear
+from oracle import matmul_ref
+from tests.gguf_cases import NAMES, Q4_K, Q6_K, Q8_0, TYPES, activations, check_close, quantized
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(qtype, n, k, m, seed=0, bias=None):
+    blocks, w = quantized(qtype, n, k, seed)
+    x = activations(m, k, seed, torch.bfloat16)
+    ref = matmul_ref.linear_ref(x.float().numpy(), w)
+    y = gguf_gemm(x.cuda(), torch.from_numpy(blocks).cuda(), qtype, (n, k), bias=bias).cpu().numpy()
+    return y, ref
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_gemm_tile_edges(qtype):
+    qk = 256 if qtype in (Q4_K, Q6_K) else 32
+    for n, k, m in ((1, qk, 1), (130, 2 * qk, 129), (257, 3 * qk, 17), (64, 8 * qk, 300)):
+        print(f"gemm {NAMES[qtype]} [{n},{k}] m={m}", flush=True)
+        y, ref = _run(qtype, n, k, m, seed=n + m)
+        check_close(y, ref, f"gemm {NAMES[qtype]} [{n},{k}] m={m}")
+
+
+@pytest.mark.parametrize("n,k", [(14336, 4096), (4096, 14336)])
+def test_gemm_prefill_q4k_full_shape(n, k):
+    print(f"gemm Q4_K [{n},{k}] m=512", flush=True)
+    y, ref = _run(Q4_K, n, k, 512, seed=1)
+    check_close(y, ref, f"gemm Q4_K [{n},{k}] m=512")
+
+
+def test_gemm_via_linear_dispatch_and_bias():
+    blocks, w = quantized(Q6_K, 512, 1024, 4)
+    x = activations(40, 1024, 4, torch.bfloat16)
+    b = torch.from_numpy(np.random.default_rng(4).standard_normal(512, dtype=np.float32))
+    y = gguf_linear(x.cuda(), torch.from_numpy(blocks).cuda(), Q6_K, (512, 1024), bias=b.cuda()).cpu().numpy()
+    ref = matmul_ref.linear_ref(x.float().numpy(), w) + b.numpy()
+    check_close(y, ref, "linear bf16 m=40")
+
+
+def test_gemm_q8_0_k_not_multiple_of_64():
+    y, ref = _run(Q8_0, 96, 96, 70, seed=8)
+    check_close(y, ref, "gemm Q8_0 K=96")

@@ -1,0 +1,78 @@
+"""GPU parity: fused dequant-GEMV (decode, M = 1..16) against the oracle's
+fp64 dequant-then-matmul, max elementwise relative error <= 1e-3."""
+
+import numpy as np
+import pytest
+import torch
+
+from dracort_amd.kernels import gguf_gemv, gguf_linear
+from oracle import matmul_ref
+from tests.gguf_cases import NAMES, Q4_0, Q4_K, Q6_K, Q8_0, TYPES, activations, check_close, quantized
+
+pytestmark = pytest.mark.gpu
+
+# Llama-3-8B projection shapes [N, K]: q/o, k/v, gate/up, down
+LLAMA = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
+
+
+def _run(qtype, n, k, m, xdtype, seed=0, bias=False):
+    blocks, w = quantized(qtype, n, k, seed)
+    x = activations(m, k, seed, xdtype)
+    ref = matmul_ref.linear_ref(x.float().numpy(), w)
+    b = None
+    if bias:
+        b = torch.from_numpy(np.random.default_rng(seed).standard_normal(n, dtype=np.float32))
+        ref = ref + b.numpy().astype(np.float64)
+        b = b.cuda()
+    q = torch.from_numpy(blocks).cuda()
+    y = gguf_gemv(x.cuda(), q, qtype, (n, k), bias=b).cpu().numpy()
+    return y, ref
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("xdtype", [torch.float32, torch.bfloat16])
+def test_gemv_llama_shapes(qtype, xdtype):
+    for n, k in LLAMA:
+        for m in (1, 4, 8, 16):
+            print(f"gemv {NAMES[qtype]} [{n},{k}] m={m} {xdtype}", flush=True)
+            y, ref = _run(qtype, n, k, m, xdtype)
+            check_close(y, ref, f"{NAMES[qtype]} [{n},{k}] m={m} {xdtype}")
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_gemv_every_m_and_ragged_shapes(qtype):
+    qk = 256 if qtype in (Q4_K, Q6_K) else 32
+    for n, k in ((1, qk), (7, 3 * qk), (33, 5 * qk), (130, 2 * qk)):
+        for m in range(1, 17):
+            xd = torch.bfloat16 if m % 2 else torch.float32
+            print(f"gemv {NAMES[qtype]} [{n},{k}] m={m}", flush=True)
+            y, ref = _run(qtype, n, k, m, xd, seed=n * 31 + m)
+            check_close(y, ref, f"{NAMES[qtype]} [{n},{k}] m={m}")
+
+
+def test_gemv_bias_and_q6k_upstream_layout():
+    y, ref = _run(Q4_K, 512, 1024, 3, torch.float32, seed=5, bias=True)
+    check_close(y, ref, "bias")
+    y, ref = _run(Q6_K | 0x100, 300, 2048, 2, torch.bfloat16, seed=6)
+    check_close(y, ref, "q6k d-last")
+
+
+def test_linear_dispatch_large_m_float32():
+    """M > 16 with float32 activations runs as 16-row GEMV tiles."""
+    blocks, w = quantized(Q8_0, 256, 512, 9)
+    x = activations(37, 512, 9, torch.float32)
+    y = gguf_linear(x.cuda(), torch.from_numpy(blocks).cuda(), Q8_0, (256, 512)).cpu().numpy()
+    check_close(y, matmul_ref.linear_ref(x.numpy(), w), "linear f32 m=37")
+
+
+def test_gemv_batched_decode_equals_sequential():
+    """Rows of a batched GEMV equal single-row GEMVs (the reference's
+    batched-decode == sequential-decode property, tests/runtime_cpu/
+    test_batching_and_speculative.py:55-80)."""
+    blocks, _ = quantized(Q4_K, 1024, 4096, 2)
+    q = torch.from_numpy(blocks).cuda()
+    x = activations(8, 4096, 2, torch.bfloat16).cuda()
+    yb = gguf_gemv(x, q, Q4_K, (1024, 4096))
+    for i in range(8):
+        yi = gguf_gemv(x[i:i + 1].contiguous(), q, Q4_K, (1024, 4096))
+        assert torch.allclose(yb[i], yi[0], rtol=1e-5, atol=1e-5)

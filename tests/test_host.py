@@ -1,0 +1,165 @@
+"""Host-side tests (no GPU): the C ABI library loads and exports every symbol
+the header declares, argument errors map onto the reference's exception
+classes without launching anything, and the host logic (quantizers, format
+helpers, backend registry) behaves."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from dracort_amd import _native
+from dracort_amd.exceptions import DracoFormatError
+from dracort_amd.format import gguf as fmt
+from oracle import gguf_ref
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "draco_gguf.h")
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(draco_gguf_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    declared = _declared_symbols()
+    assert len(declared) >= 9
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_native.SIGNATURES), "ctypes signatures must cover the header exactly"
+    assert lib.draco_gguf_abi_version() == _native.ABI_VERSION
+
+
+@pytest.mark.parametrize("qtype,expect", [(2, (32, 18)), (8, (32, 34)), (12, (256, 144)), (14, (256, 210)),
+                                          (14 | 0x100, (256, 210))])
+def test_block_info(qtype, expect):
+    assert _native.block_info(qtype) == expect
+    assert fmt.layout(qtype) == expect
+
+
+def test_block_info_rejects_unknown_types():
+    for bad in (0, 1, 3, 16, 8 | 0x100):
+        with pytest.raises(DracoFormatError):
+            _native.block_info(bad)
+
+
+FAKE = 0x10000  # aligned, never dereferenced: every call below fails validation first
+
+
+def _dq(qtype, blocks, nbytes, out, n, k):
+    return _native.load().draco_gguf_dequant_f32(qtype, blocks, nbytes, out, n, k, None)
+
+
+def test_error_codes_before_launch():
+    lib = _native.load()
+    assert _dq(16, FAKE, 1 << 20, FAKE, 4, 256) == _native.DRACO_EINVAL_QTYPE
+    assert "not supported" in _native.last_error()
+    assert _dq(12, FAKE, 1 << 20, FAKE, 4, 300) == _native.DRACO_EINVAL_SHAPE          # K % 256
+    assert _dq(12, FAKE, 4 * 144 - 1, FAKE, 4, 256) == _native.DRACO_EINVAL_SHAPE      # truncated payload
+    assert "bytes" in _native.last_error()
+    assert _dq(12, None, 1 << 20, FAKE, 4, 256) == _native.DRACO_EINVAL_ARG            # NULL
+    assert _dq(12, FAKE + 4, 1 << 20, FAKE, 4, 256) == _native.DRACO_EINVAL_ARG        # misaligned
+    assert _dq(12, FAKE, 1 << 20, FAKE, 0, 256) == _native.DRACO_EINVAL_SHAPE          # empty
+    gemv = lib.draco_gguf_gemv
+    assert gemv(12, FAKE, 1 << 20, FAKE, 1, None, FAKE, 17, 4, 256, None) == _native.DRACO_EINVAL_SHAPE  # M > 16
+    assert gemv(12, FAKE, 1 << 20, FAKE, 1, None, FAKE, 0, 4, 256, None) == _native.DRACO_EINVAL_SHAPE
+    assert gemv(12, FAKE, 1 << 20, FAKE, 7, None, FAKE, 1, 4, 256, None) == _native.DRACO_EINVAL_ARG    # dtype
+    assert lib.draco_gguf_gemm(8, FAKE, 10, FAKE, None, FAKE, 64, 4, 64, None) == _native.DRACO_EINVAL_SHAPE
+    ptrs = (ctypes.c_void_p * 2)(FAKE, FAKE)
+    moe = lib.draco_gguf_moe_ffn
+    args = [12, ptrs, ptrs, ptrs, 1 << 30, FAKE, FAKE, 1, FAKE, 64, 256, 512, 2, 2, FAKE, 1 << 30, None]
+    bad_k = list(args)
+    bad_k[13] = 3  # top_k > n_experts
+    assert moe(*bad_k) == _native.DRACO_EINVAL_SHAPE
+    small_ws = list(args)
+    small_ws[15] = 16
+    assert moe(*small_ws) == _native.DRACO_EWORKSPACE
+    trunc = list(args)
+    trunc[4] = 100
+    assert moe(*trunc) == _native.DRACO_EINVAL_SHAPE
+    assert lib.draco_gguf_moe_workspace_size(64, 4096, 14336, 8, 2) > 64 * 2 * (4096 + 14336) * 4
+
+
+def test_check_maps_codes_to_reference_exceptions():
+    _dq(16, FAKE, 1 << 20, FAKE, 4, 256)
+    with pytest.raises(DracoFormatError):
+        _native.check(_native.DRACO_EINVAL_QTYPE, "x")
+    with pytest.raises(ValueError):
+        _native.check(_native.DRACO_EINVAL_ARG, "x")
+    from dracort_amd.exceptions import KernelError
+    with pytest.raises(KernelError):
+        _native.check(_native.DRACO_EHIP, "x")
+
+
+def test_operators_refuse_cpu_tensors():
+    from dracort_amd.kernels import gguf_dequantize, gguf_linear
+    q = torch.zeros(144, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="GPU"):
+        gguf_dequantize(q, 12, (1, 256))
+    with pytest.raises(ValueError, match="GPU"):
+        gguf_linear(torch.zeros(1, 256), q, 12, (1, 256))
+
+
+def test_format_helpers():
+    assert fmt.row_bytes(12, 4096) == 16 * 144
+    assert fmt.tensor_bytes(14, (4096, 14336)) == 4096 * 56 * 210
+    with pytest.raises(DracoFormatError):
+        fmt.row_bytes(2, 48)
+    assert fmt.BITS_PER_WEIGHT[12] == 4.5
+
+
+# --- quantizers (product code, run on the CPU here) ---------------------------
+
+def test_q8_0_q4_0_quantizers_reproduce_reference_encoder_bytes():
+    from dracort_amd.quantization import quantize_q4_0, quantize_q8_0
+    z = np.load(os.path.join(GOLDEN, "gguf_encoder_golden.npz"))
+    for tag in ("small", "wide", "zero"):
+        x = torch.from_numpy(z[f"x_{tag}"]).reshape(-1, 32)
+        assert np.array_equal(quantize_q8_0(x).numpy(), z[f"q8_0_{tag}"])
+        assert np.array_equal(quantize_q4_0(x).numpy(), z[f"q4_0_{tag}"])
+
+
+@pytest.mark.parametrize("qtype,tol", [(12, 0.6), (14, 0.55)])
+def test_k_quantizers_round_trip(qtype, tol):
+    """Error per element within `tol` quantization steps of its sub-block."""
+    from dracort_amd.quantization import quantize
+    rng = np.random.default_rng(1)
+    w = (rng.normal(size=(16, 1024)) * 0.02).astype(np.float32)
+    w[3] *= 4.0
+    blocks = quantize(torch.from_numpy(w), qtype).numpy()
+    assert blocks.size == fmt.tensor_bytes(qtype, w.shape)
+    dq = gguf_ref.dequantize_matrix(qtype, blocks, w.shape)
+    sub = 32 if qtype == 12 else 16
+    span = w.reshape(-1, sub)
+    if qtype == 12:
+        step = (span.max(1) - np.minimum(span.min(1), 0)) / 15
+    else:
+        step = np.abs(span).max(1) / 31
+    err = np.abs(dq - w).reshape(-1, sub).max(1)
+    # the 6-/8-bit rounding of the sub-block scales adds a few percent of a step
+    assert np.all(err <= tol * step + 2e-4 * np.abs(w).max()), float((err / step).max())
+
+
+def test_q6k_quantizer_d_last_layout():
+    from dracort_amd.quantization import quantize
+    w = torch.from_numpy((np.random.default_rng(2).normal(size=(4, 512)) * 0.02).astype(np.float32))
+    ref = quantize(w, 14).numpy()
+    up = quantize(w, 14 | 0x100).numpy()
+    assert np.array_equal(gguf_ref.q6k_reorder(ref, to_upstream=True), up)
+
+
+def test_registry_has_gguf_backend():
+    from dracort_amd.quantization import QUANT_REGISTRY, GGUFBackend
+    be = QUANT_REGISTRY.get("GGUF")
+    assert isinstance(be, GGUFBackend) and "gguf" in QUANT_REGISTRY
+    info = be.get_kernel_info()
+    assert info["gpu_kernel"] and info["arch"] == "gfx950"
+    assert be.supports_gpu_kernel(torch.device("cuda"))
+    assert be.estimate_memory(4096 * 4096, 4) == 4096 * 4096 * 9 // 16

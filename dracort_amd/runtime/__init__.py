@@ -1,0 +1,9 @@
+"""GPU counterpart of the reference CPU executor's projection sequence."""
+
+from dracort_amd.runtime.decode import (  # noqa: F401
+    DecodeStep,
+    LayerSet,
+    LlamaShape,
+    layer_set_bytes,
+    synthetic_layer_set,
+)

@@ -1,0 +1,156 @@
+"""Weight-streaming decode step over a Llama-style GGUF layer set.
+
+Counterpart of the reference executor's per-token projection sequence:
+``forward_step`` / ``forward_batch_decode`` run, per layer, ``_qkv`` (3x
+``_linear``), ``_o_proj`` and ``_mlp`` (gate, up, SwiGLU, down), then the
+final ``lm_head`` ``_linear`` (``draco/runtime/cpu/executor.py:208-277,
+290-396``).  Here each ``_linear`` is a fused dequant-GEMV on the GPU over the
+packed GGUF blocks, and the whole step can be captured into one HIP graph.
+
+Only the projections are modelled: attention over the KV cache and the RMS
+norms are out of this path (the attention output fed to ``o_proj`` is the q
+projection itself), so a step streams exactly the layer set's weight bytes.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional
+
+import torch
+
+from dracort_amd.format.gguf import GGML_TYPE_Q4_K, GGML_TYPE_Q6_K, tensor_bytes
+from dracort_amd.kernels.gguf import gguf_gemv
+from dracort_amd.quantization.gguf import GGUFQuantizedWeight
+from dracort_amd.quantization.quantize import quantize
+
+PROJ = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+@dataclass
+class LlamaShape:
+    hidden: int = 4096
+    inter: int = 14336
+    kv_dim: int = 1024
+    vocab: int = 128256
+    n_layers: int = 32
+
+    def proj_shape(self, name: str):
+        h, i, kv = self.hidden, self.inter, self.kv_dim
+        return {"q": (h, h), "k": (kv, h), "v": (kv, h), "o": (h, h), "gate": (i, h), "up": (i, h),
+                "down": (h, i)}[name]
+
+
+# Q4_K_M assignment used by the layer-set workload: Q4_K for attention and
+# gate/up, Q6_K for down and lm_head.
+Q4_K_M_TYPES = {"q": GGML_TYPE_Q4_K, "k": GGML_TYPE_Q4_K, "v": GGML_TYPE_Q4_K, "o": GGML_TYPE_Q4_K,
+                "gate": GGML_TYPE_Q4_K, "up": GGML_TYPE_Q4_K, "down": GGML_TYPE_Q6_K}
+
+
+@dataclass
+class LayerSet:
+    shape: LlamaShape
+    layers: List[Dict[str, GGUFQuantizedWeight]] = field(default_factory=list)
+    lm_head: Optional[GGUFQuantizedWeight] = None
+
+    @property
+    def weight_bytes(self) -> int:
+        total = sum(w.nbytes for layer in self.layers for w in layer.values())
+        return total + (self.lm_head.nbytes if self.lm_head is not None else 0)
+
+
+def synthetic_weight(n: int, k: int, ggml_type: int, gen: torch.Generator, device) -> GGUFQuantizedWeight:
+    """N(0, 0.02) weight with 1 % of its rows (seeded) scaled x4, quantized on the device."""
+    w = torch.randn((n, k), generator=gen, device=device, dtype=torch.float32).mul_(0.02)
+    rows = torch.randperm(n, generator=gen, device=device)[: max(1, n // 100)]
+    w[rows] *= 4.0
+    q = quantize(w, ggml_type)
+    del w
+    return GGUFQuantizedWeight(q, ggml_type, (n, k))
+
+
+def synthetic_layer_set(shape: LlamaShape, seed: int = 0, device="cuda", types=None,
+                        lm_head_type: int = GGML_TYPE_Q6_K) -> LayerSet:
+    types = dict(Q4_K_M_TYPES if types is None else types)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    ls = LayerSet(shape)
+    for _ in range(shape.n_layers):
+        layer = {}
+        for name in PROJ:
+            n, k = shape.proj_shape(name)
+            layer[name] = synthetic_weight(n, k, types[name], gen, device)
+        ls.layers.append(layer)
+    ls.lm_head = synthetic_weight(shape.vocab, shape.hidden, lm_head_type, gen, device)
+    return ls
+
+
+def layer_set_bytes(shape: LlamaShape, types=None, lm_head_type: int = GGML_TYPE_Q6_K) -> int:
+    types = dict(Q4_K_M_TYPES if types is None else types)
+    per_layer = sum(tensor_bytes(types[p], shape.proj_shape(p)) for p in PROJ)
+    return shape.n_layers * per_layer + tensor_bytes(lm_head_type, (shape.vocab, shape.hidden))
+
+
+class DecodeStep:
+    """Preallocated buffers + the projection chain for a batch of `m` tokens.
+
+    Activations enter as bfloat16 [m, hidden]; projection outputs and the
+    residual stream are float32; the SwiGLU product stays float32 (as the
+    reference's numpy ``swiglu``).
+    """
+
+    def __init__(self, ls: LayerSet, m: int = 1, device="cuda") -> None:
+        s = ls.shape
+        self.ls, self.m = ls, m
+        f32 = dict(dtype=torch.float32, device=device)
+        self.x_in = torch.randn((m, s.hidden), generator=torch.Generator(device=device).manual_seed(1234),
+                                device=device, dtype=torch.float32).to(torch.bfloat16)
+        self.h = torch.empty((m, s.hidden), **f32)
+        self.q = torch.empty((m, s.hidden), **f32)
+        self.k = torch.empty((m, s.kv_dim), **f32)
+        self.v = torch.empty((m, s.kv_dim), **f32)
+        self.o = torch.empty((m, s.hidden), **f32)
+        self.g = torch.empty((m, s.inter), **f32)
+        self.u = torch.empty((m, s.inter), **f32)
+        self.d = torch.empty((m, s.hidden), **f32)
+        self.logits = torch.empty((m, s.vocab), **f32)
+        self.graph: Optional[torch.cuda.CUDAGraph] = None
+
+    def _lin(self, x, w: GGUFQuantizedWeight, out):
+        return gguf_gemv(x, w.data, w.ggml_type, w.shape, out=out)
+
+    def run(self) -> torch.Tensor:
+        self.h.copy_(self.x_in)
+        x = self.x_in
+        for layer in self.ls.layers:
+            self._lin(x, layer["q"], self.q)
+            self._lin(x, layer["k"], self.k)
+            self._lin(x, layer["v"], self.v)
+            self._lin(self.q, layer["o"], self.o)
+            self.h.add_(self.o)
+            self._lin(self.h, layer["gate"], self.g)
+            self._lin(self.h, layer["up"], self.u)
+            torch.nn.functional.silu(self.g, inplace=True)
+            self.g.mul_(self.u)
+            self._lin(self.g, layer["down"], self.d)
+            self.h.add_(self.d)
+            x = self.h
+        self._lin(self.h, self.ls.lm_head, self.logits)
+        return self.logits
+
+    def capture(self) -> None:
+        """Capture one step into a HIP graph (replay with ``replay``)."""
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self.run()  # warm the allocator / library outside capture
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.run()
+        self.graph = g
+
+    def replay(self) -> torch.Tensor:
+        assert self.graph is not None
+        self.graph.replay()
+        return self.logits

@@ -29,7 +29,7 @@ DRACO_DTYPE_F32 = 0
 DRACO_DTYPE_BF16 = 1
 DRACO_GGUF_Q6K_D_LAST = 0x100
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _c_int, _c_i64, _c_size, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
 
@@ -40,6 +40,13 @@ SIGNATURES = {
     "draco_gguf_block_info": (_c_int, [_c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
     "draco_gguf_dequant_f32": (_c_int, [_c_int, _vp, _c_size, _vp, _c_i64, _c_i64, _vp]),
     "draco_gguf_gemv": (_c_int, [_c_int, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
+    "draco_gguf_gemv_multi": (
+        _c_int,
+        [_c_int, _c_int, ctypes.POINTER(_vp), ctypes.POINTER(_c_size), ctypes.POINTER(_c_i64), ctypes.POINTER(_vp),
+         ctypes.POINTER(_vp), _vp, _c_int, _c_i64, _c_i64, _vp],
+    ),
+    "draco_gguf_gemv_swiglu": (_c_int, [_c_int, _vp, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
+    "draco_gguf_gemv_residual": (_c_int, [_c_int, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "draco_gguf_gemm": (_c_int, [_c_int, _vp, _c_size, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "draco_gguf_linear": (_c_int, [_c_int, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "draco_gguf_moe_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),

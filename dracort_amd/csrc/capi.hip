@@ -76,6 +76,13 @@ int check_bytes(const TypeInfo& t, int64_t n, int64_t k, size_t have, const char
   return DRACO_OK;
 }
 
+// [a, a + na) and [b, b + nb) overlap (NULL never overlaps)
+bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+  if (!a || !b) return false;
+  const uintptr_t x0 = reinterpret_cast<uintptr_t>(a), y0 = reinterpret_cast<uintptr_t>(b);
+  return x0 < y0 + nb && y0 < x0 + na;
+}
+
 int check_ptr(const void* p, const char* name) {
   if (p == nullptr) return set_error(DRACO_EINVAL_ARG, "%s is NULL", name);
   if (!aligned16(p)) return set_error(DRACO_EINVAL_ARG, "%s is not 16-byte aligned", name);
@@ -89,7 +96,7 @@ using namespace draco;
 
 extern "C" {
 
-int draco_gguf_abi_version(void) { return 1; }
+int draco_gguf_abi_version(void) { return 2; }
 
 const char* draco_gguf_last_error(void) { return g_last_error; }
 
@@ -129,6 +136,92 @@ int draco_gguf_gemv(int ggml_type, const void* w, size_t w_bytes, const void* x,
   if (int rc = check_ptr(y, "y")) return rc;
   return gemv_dispatch(t.base, t.d_last, w, x, x_dtype == DRACO_DTYPE_BF16, bias, y, (int)m, (int)n, (int)k,
                        static_cast<hipStream_t>(stream));
+}
+
+int draco_gguf_gemv_multi(int ggml_type, int n_mats, const void* const* w, const size_t* w_bytes,
+                          const int64_t* n, float* const* y, void* const* y_bf16, const void* x, int x_dtype,
+                          int64_t m, int64_t k, void* stream) {
+  g_last_error[0] = 0;
+  TypeInfo t;
+  if (int rc = decode_type(ggml_type, &t)) return rc;
+  if (n_mats < 1 || n_mats > 4) return set_error(DRACO_EINVAL_ARG, "n_mats must be 1..4, got %d", n_mats);
+  if (!w || !w_bytes || !n) return set_error(DRACO_EINVAL_ARG, "w, w_bytes and n must not be NULL");
+  if (m < 1 || m > 16)
+    return set_error(DRACO_EINVAL_SHAPE, "GEMV takes 1..16 activation rows, got %lld", (long long)m);
+  if (x_dtype != DRACO_DTYPE_F32 && x_dtype != DRACO_DTYPE_BF16)
+    return set_error(DRACO_EINVAL_ARG, "unknown activation dtype %d", x_dtype);
+  if (int rc = check_ptr(x, "x")) return rc;
+  const size_t xbytes = (size_t)m * k * (x_dtype == DRACO_DTYPE_BF16 ? 2 : 4);
+  int ns[4];
+  int64_t total = 0;
+  float* ys[4] = {nullptr, nullptr, nullptr, nullptr};
+  uint16_t* ybs[4] = {nullptr, nullptr, nullptr, nullptr};
+  for (int i = 0; i < n_mats; ++i) {
+    if (int rc = check_matrix(t, n[i], k)) return rc;
+    if (int rc = check_bytes(t, n[i], k, w_bytes[i], "w[i]")) return rc;
+    if (int rc = check_ptr(w[i], "w[i]")) return rc;
+    ys[i] = y ? y[i] : nullptr;
+    ybs[i] = y_bf16 ? static_cast<uint16_t*>(y_bf16[i]) : nullptr;
+    if (!ys[i] && !ybs[i]) return set_error(DRACO_EINVAL_ARG, "matrix %d has neither y nor y_bf16", i);
+    if (ys[i] && (reinterpret_cast<uintptr_t>(ys[i]) & 3u)) return set_error(DRACO_EINVAL_ARG, "y[%d] misaligned", i);
+    if (ybs[i] && (reinterpret_cast<uintptr_t>(ybs[i]) & 1u))
+      return set_error(DRACO_EINVAL_ARG, "y_bf16[%d] misaligned", i);
+    if (overlaps(x, xbytes, ys[i], (size_t)m * n[i] * 4) || overlaps(x, xbytes, ybs[i], (size_t)m * n[i] * 2))
+      return set_error(DRACO_EINVAL_ARG, "x overlaps an output of matrix %d", i);
+    ns[i] = (int)n[i];
+    total += n[i];
+  }
+  if (total > kMaxDim) return set_error(DRACO_EINVAL_SHAPE, "too many rows in one launch");
+  return gemv_multi_dispatch(t.base, t.d_last, n_mats, w, ns, ys, ybs, x, x_dtype == DRACO_DTYPE_BF16, nullptr,
+                             (int)m, (int)k, static_cast<hipStream_t>(stream));
+}
+
+int draco_gguf_gemv_swiglu(int ggml_type, const void* w_gate, const void* w_up, size_t w_bytes, const void* x,
+                           int x_dtype, float* y, void* y_bf16, int64_t m, int64_t n, int64_t k, void* stream) {
+  g_last_error[0] = 0;
+  TypeInfo t;
+  if (int rc = decode_type(ggml_type, &t)) return rc;
+  if (int rc = check_matrix(t, n, k)) return rc;
+  if (int rc = check_bytes(t, n, k, w_bytes, "w")) return rc;
+  if (m < 1 || m > 16)
+    return set_error(DRACO_EINVAL_SHAPE, "GEMV takes 1..16 activation rows, got %lld", (long long)m);
+  if (x_dtype != DRACO_DTYPE_F32 && x_dtype != DRACO_DTYPE_BF16)
+    return set_error(DRACO_EINVAL_ARG, "unknown activation dtype %d", x_dtype);
+  if (int rc = check_ptr(w_gate, "w_gate")) return rc;
+  if (int rc = check_ptr(w_up, "w_up")) return rc;
+  if (int rc = check_ptr(x, "x")) return rc;
+  if (!y && !y_bf16) return set_error(DRACO_EINVAL_ARG, "y and y_bf16 are both NULL");
+  if ((reinterpret_cast<uintptr_t>(y) & 3u) || (reinterpret_cast<uintptr_t>(y_bf16) & 1u))
+    return set_error(DRACO_EINVAL_ARG, "y / y_bf16 misaligned");
+  const size_t xbytes = (size_t)m * k * (x_dtype == DRACO_DTYPE_BF16 ? 2 : 4);
+  if (overlaps(x, xbytes, y, (size_t)m * n * 4) || overlaps(x, xbytes, y_bf16, (size_t)m * n * 2))
+    return set_error(DRACO_EINVAL_ARG, "x overlaps an output");
+  return gemv_swiglu_dispatch(t.base, t.d_last, w_gate, w_up, y, static_cast<uint16_t*>(y_bf16), x,
+                              x_dtype == DRACO_DTYPE_BF16, (int)m, (int)n, (int)k, static_cast<hipStream_t>(stream));
+}
+
+int draco_gguf_gemv_residual(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype, float* resid,
+                             void* resid_bf16, int64_t m, int64_t n, int64_t k, void* stream) {
+  g_last_error[0] = 0;
+  TypeInfo t;
+  if (int rc = decode_type(ggml_type, &t)) return rc;
+  if (int rc = check_matrix(t, n, k)) return rc;
+  if (int rc = check_bytes(t, n, k, w_bytes, "w")) return rc;
+  if (m < 1 || m > 16)
+    return set_error(DRACO_EINVAL_SHAPE, "GEMV takes 1..16 activation rows, got %lld", (long long)m);
+  if (x_dtype != DRACO_DTYPE_F32 && x_dtype != DRACO_DTYPE_BF16)
+    return set_error(DRACO_EINVAL_ARG, "unknown activation dtype %d", x_dtype);
+  if (int rc = check_ptr(w, "w")) return rc;
+  if (int rc = check_ptr(x, "x")) return rc;
+  if (!resid || (reinterpret_cast<uintptr_t>(resid) & 3u))
+    return set_error(DRACO_EINVAL_ARG, "resid is NULL or misaligned");
+  if (reinterpret_cast<uintptr_t>(resid_bf16) & 1u) return set_error(DRACO_EINVAL_ARG, "resid_bf16 misaligned");
+  const size_t xbytes = (size_t)m * k * (x_dtype == DRACO_DTYPE_BF16 ? 2 : 4);
+  if (overlaps(x, xbytes, resid, (size_t)m * n * 4) || overlaps(x, xbytes, resid_bf16, (size_t)m * n * 2))
+    return set_error(DRACO_EINVAL_ARG, "x overlaps resid / resid_bf16");
+  return gemv_resid_dispatch(t.base, t.d_last, w, x, x_dtype == DRACO_DTYPE_BF16, resid,
+                             static_cast<uint16_t*>(resid_bf16), (int)m, (int)n, (int)k,
+                             static_cast<hipStream_t>(stream));
 }
 
 int draco_gguf_gemm(int ggml_type, const void* w, size_t w_bytes, const void* x_bf16, const float* bias, float* y,

@@ -21,6 +21,16 @@ int dequant_dispatch(int qtype, bool d_last, const void* w, float* out, int64_t 
 int gemv_dispatch(int qtype, bool d_last, const void* w, const void* x, bool x_bf16, const float* bias,
                   float* y, int m, int n, int k, hipStream_t s);
 
+int gemv_multi_dispatch(int qtype, bool d_last, int n_mats, const void* const* w, const int* n, float* const* y,
+                        uint16_t* const* yb, const void* x, bool xbf16, const float* bias, int m, int k,
+                        hipStream_t s);
+
+int gemv_swiglu_dispatch(int qtype, bool d_last, const void* w_gate, const void* w_up, float* y, uint16_t* yb,
+                         const void* x, bool xbf16, int m, int n, int k, hipStream_t s);
+
+int gemv_resid_dispatch(int qtype, bool d_last, const void* w, const void* x, bool xbf16, float* resid,
+                        uint16_t* resid_bf16, int m, int n, int k, hipStream_t s);
+
 int gemm_dispatch(int qtype, bool d_last, const void* w, const void* x_bf16, const float* bias, float* y,
                   int m, int n, int k, hipStream_t s);
 

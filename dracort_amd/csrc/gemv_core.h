@@ -7,11 +7,26 @@
 //     acc[r][m] += a_g * sum_i(code_i * x_m[pos_i]) + b_g * sum_i(x_m[pos_i])
 // so the block scale and min are applied once per group, not once per weight.
 // The activations of a unit serve all R rows.  Accumulation is float32.
+//
+// Two variants:
+//  * gemv_accumulate_lds: the activations are staged in LDS by the workgroup
+//    first, and the weight units are double-buffered in registers: the loads
+//    of unit u + 64 are issued before the math of unit u.  Because the vector
+//    memory counter retires loads in issue order, the prefetch only overlaps
+//    the math if the math reads nothing else from global memory -- hence x in
+//    LDS (whose reads are counted separately).  With bfloat16 activations the
+//    codes are turned into bf16 pairs (128 + code, exact: one v_perm_b32 per
+//    pair against the constant byte 0x43) and multiplied with
+//    v_dot2_f32_bf16; the bias 128 * sum(x) is folded into b_g.
+//  * gemv_accumulate: activations read from global memory, no prefetch; used
+//    where x does not fit in LDS (many activation rows, long K) and by MoE.
 #pragma once
 
 #include "gguf_common.h"
 
 namespace draco {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -19,8 +34,38 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes, result in every lane: DPP within rows of 16 lanes
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror),
+// then two cross-row exchanges.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
+
+__device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                         false);
+}
+
+// bf16 pair (128 + byte0, 128 + byte1) / (128 + byte2, 128 + byte3) of a dword of
+// small unsigned codes (< 128): bf16 0x43XX is exactly 128 + XX for XX < 128.
+__device__ __forceinline__ uint32_t code_pair_lo(uint32_t v) { return __builtin_amdgcn_perm(0x43434343u, v, 0x04010400u); }
+__device__ __forceinline__ uint32_t code_pair_hi(uint32_t v) { return __builtin_amdgcn_perm(0x43434343u, v, 0x04030402u); }
+constexpr float kCodeBias = 128.f;
+constexpr uint32_t kOnePair = 0x3F803F80u;  // bf16 (1.0, 1.0)
 
 // Load `GL` consecutive activations starting at element `p` of row `xr` as float.
 template <int GL, bool XBF16>
@@ -55,14 +100,19 @@ __device__ __forceinline__ void unit_coeffs(const Raw<QT>& r, int u, float* a, f
     a[0] = f16_bits_to_f32(r.d);
     b[0] = -8.f * a[0];
   } else if constexpr (QT == kQ4_K) {
+    // all eight 6-bit scales / mins as bytes (SWAR form of the reference's
+    // _scale_min), then this unit's two sub-blocks j0, j0 + 1 by byte select
     const float d = f16_bits_to_f32(r.head.x), dmin = f16_bits_to_f32(r.head.x >> 16);
+    const uint32_t s0 = r.head.y, s1 = r.head.z, s2 = r.head.w;
     const int j0 = 2 * ((u & 7) >> 1);
+    const bool hi = j0 >= 4;
+    const uint32_t scw = hi ? ((s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u)) : (s0 & 0x3F3F3F3Fu);
+    const uint32_t mw = hi ? (((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u)) : (s1 & 0x3F3F3F3Fu);
+    const int sh = 8 * (j0 & 3);
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-      uint32_t sc, mn;
-      q4k_scale_min(r.head, j0 + g, sc, mn);
-      a[g] = d * (float)sc;
-      b[g] = -(dmin * (float)mn);
+      a[g] = d * (float)((scw >> (sh + 8 * g)) & 0xFFu);
+      b[g] = -(dmin * (float)((mw >> (sh + 8 * g)) & 0xFFu));
     }
   } else {
     const float d = f16_bits_to_f32(r.d);
@@ -93,6 +143,21 @@ __device__ __forceinline__ float unit_code(const Raw<QT>& r, int g, int i) {
   }
 }
 
+// Dword j (codes 4j .. 4j+3, one per byte) of group g, unsigned codes only.
+template <int QT>
+__device__ __forceinline__ uint32_t unit_code_dword(const Raw<QT>& r, int g, int j) {
+  if constexpr (QT == kQ4_0) {
+    return j < 4 ? nib_lo(r.q[j]) : nib_hi(r.q[j - 4]);
+  } else if constexpr (QT == kQ4_K) {
+    const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+    return g == 0 ? nib_lo(q[j]) : nib_hi(q[j]);
+  } else {
+    return q6_codes(g, r.qla[j], r.qlb[j], r.qh[j]);
+  }
+}
+
+// Formats whose codes are small unsigned integers (bf16 dot2 path).
+template <int QT> struct UnsignedCodes { static constexpr bool value = QT != kQ8_0; };
 
 // acc[r][mi] (lane partial sums) for rows n0 .. n0+R-1 and activation rows
 // 0 .. m-1 (m <= MT); xrow(mi) returns the address of activation row mi.
@@ -142,6 +207,277 @@ __device__ __forceinline__ void gemv_accumulate(const uint8_t* __restrict__ w, i
         }
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LDS-staged activations + double-buffered weight units
+// ---------------------------------------------------------------------------
+
+// Copies activation rows 0..m-1 (rows m..MT-1 zero) into LDS as MT rows of k
+// elements; all threads of the workgroup must call it (it ends in a barrier).
+template <int MT, bool XBF16, class XRow>
+__device__ __forceinline__ void stage_x_lds(uint4* lds, int m, int k, XRow xrow) {
+  constexpr int XB = XBF16 ? 2 : 4;
+  const int chunks = k * XB / 16;
+  for (int i = threadIdx.x; i < MT * chunks; i += blockDim.x) {
+    const int mi = i / chunks, c = i - mi * chunks;
+    uint4 v = {0u, 0u, 0u, 0u};
+    if (mi < m) v = reinterpret_cast<const uint4*>(xrow(mi))[c];
+    lds[i] = v;
+  }
+  __syncthreads();
+}
+
+// Permuted LDS layout of staged activations (used when K is a whole number of
+// 2048-element steps): within each step, the j-th 16-byte chunk that lane l
+// reads for its unit (unit index l inside the step) is stored at slot
+// j * 64 + l, so each LDS read instruction of a wave covers 1 KB contiguous
+// (no bank conflicts).  CE = elements per 16-byte chunk.
+template <bool XBF16> struct XChunk { static constexpr int CE = XBF16 ? 8 : 4; };
+
+// Natural element offset (within a step) of chunk j of lane l.
+template <int QT, bool XBF16>
+__device__ __forceinline__ int perm_natural_pos(int l, int j) {
+  constexpr int CE = XChunk<XBF16>::CE, GL = Fmt<QT>::GL;
+  const int e = j * CE;
+  return group_pos<QT>(l, e / GL) + (e % GL);
+}
+
+template <int QT, int MT, bool XBF16, class XRow>
+__device__ __forceinline__ void stage_x_lds_perm(uint4* lds, int m, int k, XRow xrow) {
+  constexpr int CE = XChunk<XBF16>::CE, XB = XBF16 ? 2 : 4;
+  constexpr int JPS = 32 / CE;  // chunks per lane per step
+  const int chunks = k / CE;    // per activation row
+  for (int i = threadIdx.x; i < MT * chunks; i += blockDim.x) {
+    const int mi = i / chunks, c = i - mi * chunks;
+    const int step = c / (64 * JPS), q = c - step * 64 * JPS;
+    const int j = q >> 6, l = q & 63;
+    uint4 v = {0u, 0u, 0u, 0u};
+    if (mi < m) {
+      const int p = step * 2048 + perm_natural_pos<QT, XBF16>(l, j);
+      v = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(xrow(mi)) + (size_t)p * XB);
+    }
+    lds[i] = v;
+  }
+  __syncthreads();
+}
+
+// Group sums from the permuted layout, [mi][unit][g]; ends in a barrier.
+template <int QT, int MT, bool XBF16>
+__device__ __forceinline__ void stage_group_sums_perm(const uint4* __restrict__ xs, float* __restrict__ xsum, int m,
+                                                      int k) {
+  constexpr int G = Fmt<QT>::G, GL = Fmt<QT>::GL, CE = XChunk<XBF16>::CE;
+  constexpr int CPG = GL / CE;  // chunks per group
+  const int units = k >> 5;
+  for (int i = threadIdx.x; i < MT * units * G; i += blockDim.x) {
+    const int mi = i / (units * G), rem = i - mi * units * G;
+    const int u = rem / G, g = rem - u * G;
+    float t = 0.f;
+    if (mi < m) {
+      const int step = u >> 6, l = u & 63;
+      const uint4* base = xs + ((size_t)mi * k + (size_t)step * 2048) / CE;
+#pragma unroll
+      for (int jj = 0; jj < CPG; ++jj) {
+        const uint4 v = base[(g * CPG + jj) * 64 + l];
+        if constexpr (XBF16) {
+          t += bf16_lo(v.x) + bf16_hi(v.x) + bf16_lo(v.y) + bf16_hi(v.y) + bf16_lo(v.z) + bf16_hi(v.z) +
+               bf16_lo(v.w) + bf16_hi(v.w);
+        } else {
+          t += __uint_as_float(v.x) + __uint_as_float(v.y) + __uint_as_float(v.z) + __uint_as_float(v.w);
+        }
+      }
+    }
+    xsum[i] = t;
+  }
+  __syncthreads();
+}
+
+template <int QT, bool DL, int R>
+__device__ __forceinline__ void load_rows(Raw<QT> (&dst)[R], const uint8_t* __restrict__ w, int64_t row_bytes,
+                                          int n0, int n, int u) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = n0 + r < n ? n0 + r : n - 1;
+    dst[r] = load_unit<QT, DL>(w, (int64_t)row * row_bytes, u);
+  }
+}
+
+// One 32-weight unit of R rows against MT activation rows.  xs: activation
+// rows (LDS or global), row stride k elements.  XPRE: xsum holds the
+// per-group activation sums of every unit ([mi][unit][g], row stride
+// units * G floats); otherwise they are summed here.
+template <int QT, int MT, bool XBF16, int R, bool XPRE = false, bool PERM = false>
+__device__ __forceinline__ void unit_math_lds(const Raw<QT> (&raw)[R], int u, int m, int k,
+                                              const uint4* __restrict__ xs, float (&acc)[R][MT],
+                                              const float* __restrict__ xsum = nullptr) {
+  using F = Fmt<QT>;
+  constexpr int G = F::G, GL = F::GL;
+  const int units = k >> 5;
+  // PERM: chunk c (16 bytes) of this unit's activations is at uint4 slot
+  // (row base + step base) / CE + c * 64 + (u & 63)
+  auto xchunk = [&](int mi, int c) -> const uint4* {
+    constexpr int CE = XChunk<XBF16>::CE;
+    return xs + ((size_t)mi * k + (size_t)(u >> 6) * 2048) / CE + c * 64 + (u & 63);
+  };
+  float a[R][G], b[R][G];
+#pragma unroll
+  for (int r = 0; r < R; ++r) unit_coeffs<QT>(raw[r], u, a[r], b[r]);
+
+  if constexpr (XBF16 && UnsignedCodes<QT>::value) {
+    // bf16 code pairs of every row, shared by all activation rows
+    uint32_t cp[R][G][GL / 2];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < GL / 4; ++j) {
+          const uint32_t c = unit_code_dword<QT>(raw[r], g, j);
+          cp[r][g][2 * j] = code_pair_lo(c);
+          cp[r][g][2 * j + 1] = code_pair_hi(c);
+        }
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) {
+      if (mi < m) {
+        const uint32_t* xrow = reinterpret_cast<const uint32_t*>(xs) + (size_t)mi * (k >> 1);
+        float xsg[G];
+        if constexpr (XPRE) {
+          const float* p = xsum + ((size_t)mi * units + u) * G;
+          if constexpr (G == 4) {
+            const float4 v = *reinterpret_cast<const float4*>(p);
+            xsg[0] = v.x; xsg[1] = v.y; xsg[2] = v.z; xsg[3] = v.w;
+          } else if constexpr (G == 2) {
+            const float2 v = *reinterpret_cast<const float2*>(p);
+            xsg[0] = v.x; xsg[1] = v.y;
+          } else {
+            xsg[0] = p[0];
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          uint32_t xw[GL / 2];
+#pragma unroll
+          for (int j = 0; j < GL / 8; ++j) {
+            const uint4 v = PERM ? *xchunk(mi, g * (GL / 8) + j)
+                                 : reinterpret_cast<const uint4*>(xrow + (group_pos<QT>(u, g) >> 1))[j];
+            xw[4 * j] = v.x; xw[4 * j + 1] = v.y; xw[4 * j + 2] = v.z; xw[4 * j + 3] = v.w;
+          }
+          if constexpr (!XPRE) {
+            float t = 0.f;
+#pragma unroll
+            for (int j = 0; j < GL / 2; ++j) t = dot2bf(xw[j], kOnePair, t);
+            xsg[g] = t;
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            float dot = 0.f;
+#pragma unroll
+            for (int j = 0; j < GL / 2; ++j) dot = dot2bf(cp[r][g][j], xw[j], dot);
+            acc[r][mi] = fmaf(a[r][g], dot, acc[r][mi]);
+            acc[r][mi] = fmaf(b[r][g] - kCodeBias * a[r][g], xsg[g], acc[r][mi]);
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) {
+      if (mi < m) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float xv[GL];
+          if constexpr (PERM) {
+            constexpr int CE = XChunk<XBF16>::CE;
+#pragma unroll
+            for (int j = 0; j < GL / CE; ++j) {
+              const uint4 v = *xchunk(mi, g * (GL / CE) + j);
+              if constexpr (XBF16) {
+                xv[8 * j + 0] = bf16_lo(v.x); xv[8 * j + 1] = bf16_hi(v.x);
+                xv[8 * j + 2] = bf16_lo(v.y); xv[8 * j + 3] = bf16_hi(v.y);
+                xv[8 * j + 4] = bf16_lo(v.z); xv[8 * j + 5] = bf16_hi(v.z);
+                xv[8 * j + 6] = bf16_lo(v.w); xv[8 * j + 7] = bf16_hi(v.w);
+              } else {
+                xv[4 * j + 0] = __uint_as_float(v.x); xv[4 * j + 1] = __uint_as_float(v.y);
+                xv[4 * j + 2] = __uint_as_float(v.z); xv[4 * j + 3] = __uint_as_float(v.w);
+              }
+            }
+          } else if constexpr (XBF16) {
+            load_x<GL, true>(reinterpret_cast<const uint16_t*>(xs) + (size_t)mi * k, group_pos<QT>(u, g), xv);
+          } else {
+            load_x<GL, false>(reinterpret_cast<const float*>(xs) + (size_t)mi * k, group_pos<QT>(u, g), xv);
+          }
+          float xsum_g = 0.f;
+          if constexpr (QT != kQ8_0) {
+            if constexpr (XPRE) {
+              xsum_g = xsum[((size_t)mi * units + u) * G + g];
+            } else {
+#pragma unroll
+              for (int i = 0; i < GL; ++i) xsum_g += xv[i];
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            float dot = 0.f;
+#pragma unroll
+            for (int i = 0; i < GL; ++i) dot = fmaf(unit_code<QT>(raw[r], g, i), xv[i], dot);
+            acc[r][mi] = fmaf(a[r][g], dot, acc[r][mi]);
+            if constexpr (QT != kQ8_0) acc[r][mi] = fmaf(b[r][g], xsum_g, acc[r][mi]);
+          }
+        }
+      }
+    }
+  }
+}
+
+// Per-group activation sums of every unit, [mi][unit][g] (mi < MT; zero for
+// mi >= m), from activations already staged in LDS; ends in a barrier.
+template <int QT, int MT, bool XBF16>
+__device__ __forceinline__ void stage_group_sums(const uint4* __restrict__ xs, float* __restrict__ xsum, int m,
+                                                 int k) {
+  constexpr int G = Fmt<QT>::G, GL = Fmt<QT>::GL;
+  const int units = k >> 5;
+  for (int i = threadIdx.x; i < MT * units * G; i += blockDim.x) {
+    const int mi = i / (units * G), rem = i - mi * units * G;
+    const int u = rem / G, g = rem - u * G;
+    float t = 0.f;
+    if (mi < m) {
+      float xv[GL];
+      if constexpr (XBF16) {
+        load_x<GL, true>(reinterpret_cast<const uint16_t*>(xs) + (size_t)mi * k, group_pos<QT>(u, g), xv);
+      } else {
+        load_x<GL, false>(reinterpret_cast<const float*>(xs) + (size_t)mi * k, group_pos<QT>(u, g), xv);
+      }
+#pragma unroll
+      for (int j = 0; j < GL; ++j) t += xv[j];
+    }
+    xsum[i] = t;
+  }
+  __syncthreads();
+}
+
+// Same contract as gemv_accumulate, activations already staged in LDS by stage_x_lds.
+template <int QT, bool DL, int MT, bool XBF16, int R>
+__device__ __forceinline__ void gemv_accumulate_lds(const uint8_t* __restrict__ w, int64_t row_bytes, int n0,
+                                                    int n, int k, int m, const uint4* __restrict__ xs,
+                                                    float (&acc)[R][MT]) {
+  const int lane = threadIdx.x & 63;
+  const int units = k >> 5;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) acc[r][mi] = 0.f;
+  Raw<QT> buf0[R], buf1[R];
+  int u = lane;
+  if (u < units) load_rows<QT, DL, R>(buf0, w, row_bytes, n0, n, u);
+  while (u < units) {
+    if (u + 64 < units) load_rows<QT, DL, R>(buf1, w, row_bytes, n0, n, u + 64);
+    unit_math_lds<QT, MT, XBF16, R>(buf0, u, m, k, xs, acc);
+    u += 64;
+    if (u >= units) break;
+    if (u + 64 < units) load_rows<QT, DL, R>(buf0, w, row_bytes, n0, n, u + 64);
+    unit_math_lds<QT, MT, XBF16, R>(buf1, u, m, k, xs, acc);
+    u += 64;
   }
 }
 

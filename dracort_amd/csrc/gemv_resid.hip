@@ -1,0 +1,25 @@
+// GEMV with the residual-add epilogue: resid += W x (float32, in place) and an
+// optional bfloat16 copy of the updated residual for the next projection.
+// Replaces _o_proj / the down projection plus the residual adds of
+// forward_step (draco/runtime/cpu/executor.py:273-277, 308-329).
+#include "gemv_stream.h"
+
+namespace draco {
+
+int gemv_resid_dispatch(int qtype, bool d_last, const void* w, const void* x, bool xbf16, float* resid,
+                        uint16_t* resid_bf16, int m, int n, int k, hipStream_t s) {
+  StreamJob job{};
+  job.n_mats = 1;
+  job.w[0] = static_cast<const uint8_t*>(w);
+  job.n[0] = n;
+  job.rows = n;
+  job.row_bytes = row_bytes_of(qtype, k);
+  job.k = k;
+  job.m = m;
+  job.x = x;
+  job.resid = resid;
+  job.resid_bf16 = resid_bf16;
+  return stream_dispatch<kResid>(qtype, d_last, job, xbf16, s);
+}
+
+}  // namespace draco

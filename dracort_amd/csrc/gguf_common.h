@@ -50,24 +50,41 @@ __device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) {
   return *reinterpret_cast<const uint32_t*>(p);
 }
 
-// 8 bytes at an even byte offset `o` from a 4-aligned base.
-__device__ __forceinline__ void ld8_even(const uint8_t* base, int64_t o, uint32_t& w0, uint32_t& w1) {
-  const uint8_t* p = base + (o & ~int64_t(3));
-  if ((o & 2) == 0) {
-    w0 = ld_u32(p);
-    w1 = ld_u32(p + 4);
-  } else {
-    uint32_t a = ld_u32(p), b = ld_u32(p + 4), c = ld_u32(p + 8);
-    w0 = __builtin_amdgcn_alignbyte(b, a, 2);
-    w1 = __builtin_amdgcn_alignbyte(c, b, 2);
+// ---------------------------------------------------------------------------
+// Byte loaders.  load_unit reads a unit through one of these:
+//   GlobalLoader  flat pointer + 64-bit offset (any row layout)
+//   BufferLoader  buffer resource (base, byte size) + a wave-uniform offset in
+//                 an SGPR (soffset) + a per-lane offset (voffset): no vector
+//                 address arithmetic, and reads past num_records return 0
+//                 instead of faulting.  Offsets are 32-bit (tensors < 2 GiB).
+// ---------------------------------------------------------------------------
+struct GlobalLoader {
+  const uint8_t* base;
+  __device__ __forceinline__ uint32_t u32(int64_t off) const {
+    return *reinterpret_cast<const uint32_t*>(base + off);
   }
+  __device__ __forceinline__ uint4 u128(int64_t off) const { return *reinterpret_cast<const uint4*>(base + off); }
+};
+
+// gfx9-family buffer descriptor word 3 (raw buffer, 32-bit data format)
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferRsrcWord3);
 }
 
-// 16-bit field at an even byte offset.
-__device__ __forceinline__ uint32_t ld16_even(const uint8_t* base, int64_t o) {
-  uint32_t w = ld_u32(base + (o & ~int64_t(3)));
-  return (o & 2) ? (w >> 16) : (w & 0xFFFFu);
-}
+struct BufferLoader {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int soff;  // wave-uniform byte offset (multiple of 4)
+  __device__ __forceinline__ uint32_t u32(int64_t off) const {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsrc, (int)off, soff, 0);
+  }
+  __device__ __forceinline__ uint4 u128(int64_t off) const {
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)off, soff, 0);
+    return uint4{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Raw unit payloads (what a lane keeps in registers for one unit)
@@ -83,75 +100,65 @@ template <> struct Raw<kQ4_K> { uint4 head; uint4 qs; };
 // Q6_K: 8 bytes of ql (low half), 8 of ql (+32), 8 of qh, 8 of scales, d
 template <> struct Raw<kQ6_K> { uint32_t qla[2], qlb[2], qh[2], sc[2]; uint32_t d; };
 
-// Absolute byte offset of the block that holds unit `u` of a row starting at `row_off`.
+// Byte offset of the block that holds unit `u` of a row starting at `row_off`.
 template <int QT>
 __device__ __forceinline__ int64_t unit_block_off(int64_t row_off, int u) {
   return row_off + (int64_t)(u / Fmt<QT>::UPB) * Fmt<QT>::BYTES;
 }
 
-template <int QT, bool Q6K_D_LAST = false>
-__device__ __forceinline__ Raw<QT> load_unit(const uint8_t* __restrict__ w, int64_t row_off, int u);
+// 8 bytes at an even offset `o` (see ld8_even) through a loader.
+template <class L>
+__device__ __forceinline__ void ld8_even_l(const L& ld, int64_t o, uint32_t& w0, uint32_t& w1) {
+  const int64_t p = o & ~int64_t(3);
+  const uint32_t a = ld.u32(p), b = ld.u32(p + 4);
+  const uint32_t c = ld.u32((o + 7) & ~int64_t(3));
+  const uint32_t sh = (uint32_t)o & 3u;
+  w0 = __builtin_amdgcn_alignbyte(b, a, sh);
+  w1 = __builtin_amdgcn_alignbyte(c, b, sh);
+}
 
-template <>
-__device__ __forceinline__ Raw<kQ8_0> load_unit<kQ8_0, false>(const uint8_t* __restrict__ w, int64_t row_off, int u) {
-  Raw<kQ8_0> r;
-  const int64_t o = row_off + (int64_t)u * 34;
-  const uint8_t* p = w + (o & ~int64_t(3));
-  uint32_t v[9];
+template <class L>
+__device__ __forceinline__ uint32_t ld16_even_l(const L& ld, int64_t o) {
+  const uint32_t w = ld.u32(o & ~int64_t(3));
+  return (o & 2) ? (w >> 16) : (w & 0xFFFFu);
+}
+
+// Unit `u` of the row at byte `row_off`.  Offsets are relative to the
+// loader's base, which must be 4-byte aligned.
+template <int QT, bool DL, class L>
+__device__ __forceinline__ Raw<QT> load_unit_l(const L& ld, int64_t row_off, int u) {
+  Raw<QT> r;
+  if constexpr (QT == kQ8_0 || QT == kQ4_0) {
+    constexpr int NB = QT == kQ8_0 ? 34 : 18, NW = QT == kQ8_0 ? 9 : 5, NQ = QT == kQ8_0 ? 8 : 4;
+    const int64_t o = row_off + (int64_t)u * NB;
+    const int64_t p = o & ~int64_t(3);
+    uint32_t v[NW];
 #pragma unroll
-  for (int i = 0; i < 9; ++i) v[i] = ld_u32(p + 4 * i);
-  const bool odd = (o & 2) != 0;
-  r.d = odd ? (v[0] >> 16) : (v[0] & 0xFFFFu);
+    for (int i = 0; i < NW; ++i) v[i] = ld.u32(p + 4 * i);
+    const bool odd = (o & 2) != 0;
+    r.d = odd ? (v[0] >> 16) : (v[0] & 0xFFFFu);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r.q[i] = odd ? v[i + 1] : __builtin_amdgcn_alignbyte(v[i + 1], v[i], 2);
+    for (int i = 0; i < NQ; ++i) r.q[i] = odd ? v[i + 1] : __builtin_amdgcn_alignbyte(v[i + 1], v[i], 2);
+  } else if constexpr (QT == kQ4_K) {
+    const int64_t b = unit_block_off<QT>(row_off, u);
+    r.head = ld.u128(b);
+    r.qs = ld.u128(b + 16 + 16 * (u & 7));
+  } else {
+    const int64_t b = unit_block_off<QT>(row_off, u);
+    const int s = u & 7, half = s >> 2, l0 = 8 * (s & 3);
+    constexpr int QL = DL ? 0 : 2, QH = DL ? 128 : 130, SC = DL ? 192 : 194, D = DL ? 208 : 0;
+    ld8_even_l(ld, b + QL + 64 * half + l0, r.qla[0], r.qla[1]);
+    ld8_even_l(ld, b + QL + 64 * half + 32 + l0, r.qlb[0], r.qlb[1]);
+    ld8_even_l(ld, b + QH + 32 * half + l0, r.qh[0], r.qh[1]);
+    ld8_even_l(ld, b + SC + 8 * half, r.sc[0], r.sc[1]);
+    r.d = ld16_even_l(ld, b + D);
+  }
   return r;
 }
 
-template <>
-__device__ __forceinline__ Raw<kQ4_0> load_unit<kQ4_0, false>(const uint8_t* __restrict__ w, int64_t row_off, int u) {
-  Raw<kQ4_0> r;
-  const int64_t o = row_off + (int64_t)u * 18;
-  const uint8_t* p = w + (o & ~int64_t(3));
-  uint32_t v[5];
-#pragma unroll
-  for (int i = 0; i < 5; ++i) v[i] = ld_u32(p + 4 * i);
-  const bool odd = (o & 2) != 0;
-  r.d = odd ? (v[0] >> 16) : (v[0] & 0xFFFFu);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r.q[i] = odd ? v[i + 1] : __builtin_amdgcn_alignbyte(v[i + 1], v[i], 2);
-  return r;
-}
-
-template <>
-__device__ __forceinline__ Raw<kQ4_K> load_unit<kQ4_K, false>(const uint8_t* __restrict__ w, int64_t row_off, int u) {
-  Raw<kQ4_K> r;
-  const uint8_t* blk = w + unit_block_off<kQ4_K>(row_off, u);
-  r.head = *reinterpret_cast<const uint4*>(blk);
-  r.qs = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (u & 7));
-  return r;
-}
-
-template <bool D_LAST>
-__device__ __forceinline__ Raw<kQ6_K> load_unit_q6k(const uint8_t* __restrict__ w, int64_t row_off, int u) {
-  Raw<kQ6_K> r;
-  const int64_t b = unit_block_off<kQ6_K>(row_off, u);
-  const int s = u & 7, half = s >> 2, l0 = 8 * (s & 3);
-  constexpr int QL = D_LAST ? 0 : 2, QH = D_LAST ? 128 : 130, SC = D_LAST ? 192 : 194, D = D_LAST ? 208 : 0;
-  ld8_even(w, b + QL + 64 * half + l0, r.qla[0], r.qla[1]);
-  ld8_even(w, b + QL + 64 * half + 32 + l0, r.qlb[0], r.qlb[1]);
-  ld8_even(w, b + QH + 32 * half + l0, r.qh[0], r.qh[1]);
-  ld8_even(w, b + SC + 8 * half, r.sc[0], r.sc[1]);
-  r.d = ld16_even(w, b + D);
-  return r;
-}
-
-template <>
-__device__ __forceinline__ Raw<kQ6_K> load_unit<kQ6_K, false>(const uint8_t* __restrict__ w, int64_t row_off, int u) {
-  return load_unit_q6k<false>(w, row_off, u);
-}
-template <>
-__device__ __forceinline__ Raw<kQ6_K> load_unit<kQ6_K, true>(const uint8_t* __restrict__ w, int64_t row_off, int u) {
-  return load_unit_q6k<true>(w, row_off, u);
+template <int QT, bool DL = false>
+__device__ __forceinline__ Raw<QT> load_unit(const uint8_t* __restrict__ w, int64_t row_off, int u) {
+  return load_unit_l<QT, DL>(GlobalLoader{w}, row_off, u);
 }
 
 // ---------------------------------------------------------------------------

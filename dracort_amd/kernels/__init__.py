@@ -5,6 +5,9 @@ from dracort_amd.kernels.gguf import (  # noqa: F401
     gguf_dequantize,
     gguf_gemm,
     gguf_gemv,
+    gguf_gemv_multi,
+    gguf_gemv_residual,
+    gguf_gemv_swiglu,
     gguf_linear,
     gguf_moe,
     moe_workspace_bytes,
@@ -14,6 +17,9 @@ __all__ = [
     "gguf_dequantize",
     "gguf_linear",
     "gguf_gemv",
+    "gguf_gemv_multi",
+    "gguf_gemv_swiglu",
+    "gguf_gemv_residual",
     "gguf_gemm",
     "gguf_moe",
     "moe_workspace_bytes",

@@ -174,6 +174,115 @@ def gguf_gemm(x, qweight, ggml_type, shape, bias=None, out=None) -> torch.Tensor
     return out
 
 
+def _out_check(t: Optional[torch.Tensor], dtype, numel: int, name: str) -> None:
+    if t is None:
+        return
+    _need_gpu(t, name)
+    if t.dtype != dtype or t.numel() != numel:
+        raise ValueError(f"{name} must be {dtype} with {numel} elements")
+
+
+def _x_rows(x: torch.Tensor, k: int) -> int:
+    _need_gpu(x, "x")
+    if x.shape[-1] != k:
+        raise ValueError(f"x has {x.shape[-1]} features, weight expects K={k}")
+    m = x.numel() // k
+    if not 1 <= m <= GEMV_MAX_M:
+        raise ValueError(f"fused GEMVs take 1..{GEMV_MAX_M} activation rows, got {m}")
+    return m
+
+
+def gguf_gemv_multi(
+    x: torch.Tensor,
+    weights: Sequence[Tuple[torch.Tensor, int]],
+    ggml_type: int,
+    k: int,
+    outs: Sequence[Optional[torch.Tensor]],
+    outs_bf16: Optional[Sequence[Optional[torch.Tensor]]] = None,
+) -> None:
+    """One launch for several [n_i, K] weights sharing x (e.g. q, k, v).
+
+    ``weights`` = [(qweight_i, n_i)]; ``outs[i]`` float32 [m, n_i] and/or
+    ``outs_bf16[i]`` bfloat16 [m, n_i] (either may be None).
+    """
+    m = _x_rows(x, k)
+    nm = len(weights)
+    if not 1 <= nm <= 4 or len(outs) != nm or (outs_bf16 is not None and len(outs_bf16) != nm):
+        raise ValueError("1..4 weights with one output slot each")
+    outs_bf16 = list(outs_bf16) if outs_bf16 is not None else [None] * nm
+    for i, (q, n) in enumerate(weights):
+        _check_weight(q, ggml_type, (n, k))
+        _same_device(x, q)
+        if outs[i] is None and outs_bf16[i] is None:
+            raise ValueError(f"weight {i} has no output")
+        _out_check(outs[i], torch.float32, m * n, f"outs[{i}]")
+        _out_check(outs_bf16[i], torch.bfloat16, m * n, f"outs_bf16[{i}]")
+    vp = ctypes.c_void_p
+    w_arr = (vp * nm)(*[q.data_ptr() for q, _ in weights])
+    b_arr = (ctypes.c_size_t * nm)(*[q.numel() for q, _ in weights])
+    n_arr = (ctypes.c_int64 * nm)(*[int(n) for _, n in weights])
+    y_arr = (vp * nm)(*[o.data_ptr() if o is not None else None for o in outs])
+    yb_arr = (vp * nm)(*[o.data_ptr() if o is not None else None for o in outs_bf16])
+    lib = _native.load()
+    with torch.cuda.device(x.device):
+        rc = lib.draco_gguf_gemv_multi(int(ggml_type), nm, w_arr, b_arr, n_arr, y_arr, yb_arr, x.data_ptr(),
+                                       _x_dtype(x), m, k, _stream(x))
+    _native.check(rc, "gguf_gemv_multi")
+
+
+def gguf_gemv_swiglu(
+    x: torch.Tensor,
+    w_gate: torch.Tensor,
+    w_up: torch.Tensor,
+    ggml_type: int,
+    shape: Tuple[int, int],
+    out: Optional[torch.Tensor] = None,
+    out_bf16: Optional[torch.Tensor] = None,
+) -> None:
+    """silu(x @ W_gate.T) * (x @ W_up.T) into float32 ``out`` and/or bfloat16 ``out_bf16``."""
+    n, k = _check_weight(w_gate, ggml_type, shape)
+    _check_weight(w_up, ggml_type, shape)
+    if w_gate.numel() != w_up.numel():
+        raise ValueError("gate and up buffers differ in size")
+    m = _x_rows(x, k)
+    if out is None and out_bf16 is None:
+        raise ValueError("need out and/or out_bf16")
+    _out_check(out, torch.float32, m * n, "out")
+    _out_check(out_bf16, torch.bfloat16, m * n, "out_bf16")
+    _same_device(x, w_gate, w_up)
+    lib = _native.load()
+    with torch.cuda.device(x.device):
+        rc = lib.draco_gguf_gemv_swiglu(
+            int(ggml_type), w_gate.data_ptr(), w_up.data_ptr(), w_gate.numel(), x.data_ptr(), _x_dtype(x),
+            out.data_ptr() if out is not None else None, out_bf16.data_ptr() if out_bf16 is not None else None,
+            m, n, k, _stream(x),
+        )
+    _native.check(rc, "gguf_gemv_swiglu")
+
+
+def gguf_gemv_residual(
+    x: torch.Tensor,
+    qweight: torch.Tensor,
+    ggml_type: int,
+    shape: Tuple[int, int],
+    resid: torch.Tensor,
+    resid_bf16: Optional[torch.Tensor] = None,
+) -> None:
+    """resid += x @ W.T in place (float32); resid_bf16 = bf16(resid) if given."""
+    n, k = _check_weight(qweight, ggml_type, shape)
+    m = _x_rows(x, k)
+    _out_check(resid, torch.float32, m * n, "resid")
+    _out_check(resid_bf16, torch.bfloat16, m * n, "resid_bf16")
+    _same_device(x, qweight, resid)
+    lib = _native.load()
+    with torch.cuda.device(x.device):
+        rc = lib.draco_gguf_gemv_residual(
+            int(ggml_type), qweight.data_ptr(), qweight.numel(), x.data_ptr(), _x_dtype(x), resid.data_ptr(),
+            resid_bf16.data_ptr() if resid_bf16 is not None else None, m, n, k, _stream(x),
+        )
+    _native.check(rc, "gguf_gemv_residual")
+
+
 def moe_workspace_bytes(tokens: int, hidden: int, inter: int, n_experts: int, top_k: int) -> int:
     return int(_native.load().draco_gguf_moe_workspace_size(tokens, hidden, inter, n_experts, top_k))
 

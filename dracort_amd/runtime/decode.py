@@ -4,8 +4,12 @@ Counterpart of the reference executor's per-token projection sequence:
 ``forward_step`` / ``forward_batch_decode`` run, per layer, ``_qkv`` (3x
 ``_linear``), ``_o_proj`` and ``_mlp`` (gate, up, SwiGLU, down), then the
 final ``lm_head`` ``_linear`` (``draco/runtime/cpu/executor.py:208-277,
-290-396``).  Here each ``_linear`` is a fused dequant-GEMV on the GPU over the
-packed GGUF blocks, and the whole step can be captured into one HIP graph.
+290-396``).  Here a layer is four fused dequant-GEMV launches over the packed
+GGUF blocks -- q/k/v in one launch, o with the residual add, gate/up with the
+SwiGLU product, down with the residual add -- plus one for the lm_head, and
+the whole step can be captured into one HIP graph.  The projection inputs are
+bfloat16 (each launch writes the bf16 copy its consumer reads); the residual
+stream and the logits are float32.
 
 Only the projections are modelled: attention over the KV cache and the RMS
 norms are out of this path (the attention output fed to ``o_proj`` is the q
@@ -20,7 +24,7 @@ from typing import Dict, List, Optional
 import torch
 
 from dracort_amd.format.gguf import GGML_TYPE_Q4_K, GGML_TYPE_Q6_K, tensor_bytes
-from dracort_amd.kernels.gguf import gguf_gemv
+from dracort_amd.kernels.gguf import gguf_gemv, gguf_gemv_multi, gguf_gemv_residual, gguf_gemv_swiglu
 from dracort_amd.quantization.gguf import GGUFQuantizedWeight
 from dracort_amd.quantization.quantize import quantize
 
@@ -92,50 +96,42 @@ def layer_set_bytes(shape: LlamaShape, types=None, lm_head_type: int = GGML_TYPE
 
 
 class DecodeStep:
-    """Preallocated buffers + the projection chain for a batch of `m` tokens.
-
-    Activations enter as bfloat16 [m, hidden]; projection outputs and the
-    residual stream are float32; the SwiGLU product stays float32 (as the
-    reference's numpy ``swiglu``).
-    """
+    """Preallocated buffers + the projection chain for a batch of `m` tokens."""
 
     def __init__(self, ls: LayerSet, m: int = 1, device="cuda") -> None:
         s = ls.shape
         self.ls, self.m = ls, m
         f32 = dict(dtype=torch.float32, device=device)
-        self.x_in = torch.randn((m, s.hidden), generator=torch.Generator(device=device).manual_seed(1234),
-                                device=device, dtype=torch.float32).to(torch.bfloat16)
+        b16 = dict(dtype=torch.bfloat16, device=device)
+        gen = torch.Generator(device=device).manual_seed(1234)
+        self.x_in = torch.randn((m, s.hidden), generator=gen, **f32).to(torch.bfloat16)
         self.h = torch.empty((m, s.hidden), **f32)
-        self.q = torch.empty((m, s.hidden), **f32)
-        self.k = torch.empty((m, s.kv_dim), **f32)
-        self.v = torch.empty((m, s.kv_dim), **f32)
-        self.o = torch.empty((m, s.hidden), **f32)
-        self.g = torch.empty((m, s.inter), **f32)
-        self.u = torch.empty((m, s.inter), **f32)
-        self.d = torch.empty((m, s.hidden), **f32)
+        self.h_bf16 = torch.empty((m, s.hidden), **b16)
+        self.q = torch.empty((m, s.hidden), **b16)
+        self.k = torch.empty((m, s.kv_dim), **b16)
+        self.v = torch.empty((m, s.kv_dim), **b16)
+        self.s = torch.empty((m, s.inter), **b16)
         self.logits = torch.empty((m, s.vocab), **f32)
         self.graph: Optional[torch.cuda.CUDAGraph] = None
 
-    def _lin(self, x, w: GGUFQuantizedWeight, out):
-        return gguf_gemv(x, w.data, w.ggml_type, w.shape, out=out)
-
     def run(self) -> torch.Tensor:
+        s = self.ls.shape
         self.h.copy_(self.x_in)
-        x = self.x_in
+        self.h_bf16.copy_(self.x_in)
         for layer in self.ls.layers:
-            self._lin(x, layer["q"], self.q)
-            self._lin(x, layer["k"], self.k)
-            self._lin(x, layer["v"], self.v)
-            self._lin(self.q, layer["o"], self.o)
-            self.h.add_(self.o)
-            self._lin(self.h, layer["gate"], self.g)
-            self._lin(self.h, layer["up"], self.u)
-            torch.nn.functional.silu(self.g, inplace=True)
-            self.g.mul_(self.u)
-            self._lin(self.g, layer["down"], self.d)
-            self.h.add_(self.d)
-            x = self.h
-        self._lin(self.h, self.ls.lm_head, self.logits)
+            q, k, v, o = layer["q"], layer["k"], layer["v"], layer["o"]
+            if q.ggml_type == k.ggml_type == v.ggml_type:
+                gguf_gemv_multi(self.h_bf16, [(q.data, q.shape[0]), (k.data, k.shape[0]), (v.data, v.shape[0])],
+                                q.ggml_type, s.hidden, [None, None, None], [self.q, self.k, self.v])
+            else:
+                for w, out in ((q, self.q), (k, self.k), (v, self.v)):
+                    gguf_gemv_multi(self.h_bf16, [(w.data, w.shape[0])], w.ggml_type, s.hidden, [None], [out])
+            gguf_gemv_residual(self.q, o.data, o.ggml_type, o.shape, self.h, self.h_bf16)
+            g, u, d = layer["gate"], layer["up"], layer["down"]
+            gguf_gemv_swiglu(self.h_bf16, g.data, u.data, g.ggml_type, g.shape, out_bf16=self.s)
+            gguf_gemv_residual(self.s, d.data, d.ggml_type, d.shape, self.h, self.h_bf16)
+        w = self.ls.lm_head
+        gguf_gemv(self.h_bf16, w.data, w.ggml_type, w.shape, out=self.logits)
         return self.logits
 
     def capture(self) -> None:

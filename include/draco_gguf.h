@@ -88,6 +88,41 @@ int draco_gguf_gemv(int ggml_type, const void* w, size_t w_bytes, const void* x,
                     float* y, int64_t m, int64_t n, int64_t k, void* stream);
 
 /*
+ * Several decode GEMVs sharing one activation, in one launch (e.g. the q, k
+ * and v projections of a layer):
+ *   y_i[m, n_i] = x[m, k] . W_i[n_i, k]^T   for i < n_mats (1..4),
+ * every W_i of the same ggml type and row length k, w_bytes[i] its buffer
+ * size.  y[i] (float32) and y_bf16[i] (bfloat16 copy, round to nearest even)
+ * may each be NULL but not both; y and y_bf16 themselves may be NULL arrays.
+ * 1 <= m <= 16.  x must not overlap any output.  Replaces _qkv
+ * (draco/runtime/cpu/executor.py:243-271), three _linear calls sharing x.
+ */
+int draco_gguf_gemv_multi(int ggml_type, int n_mats, const void* const* w, const size_t* w_bytes,
+                          const int64_t* n, float* const* y, void* const* y_bf16, const void* x, int x_dtype,
+                          int64_t m, int64_t k, void* stream);
+
+/*
+ * Gate and up projections with the SwiGLU product fused in:
+ *   y[m, n] = silu(x . W_gate^T) * (x . W_up^T),  silu(g) = g / (1 + e^-g),
+ * W_gate and W_up [n, k] of one ggml type, each w_bytes long; y float32 and/or
+ * y_bf16 (either may be NULL, not both); 1 <= m <= 16; x must not overlap an
+ * output.  Replaces the gate/up _linear calls and swiglu of _mlp
+ * (draco/runtime/cpu/executor.py:208-224, draco/runtime/cpu/ops.py:19-27).
+ */
+int draco_gguf_gemv_swiglu(int ggml_type, const void* w_gate, const void* w_up, size_t w_bytes, const void* x,
+                           int x_dtype, float* y, void* y_bf16, int64_t m, int64_t n, int64_t k, void* stream);
+
+/*
+ * Projection plus residual add, in place:
+ *   resid[m, n] += x . W^T,  then resid_bf16 = bf16(resid) if not NULL.
+ * 1 <= m <= 16; x must not overlap resid or resid_bf16.  Replaces _o_proj /
+ * the down projection of _mlp and the residual adds of forward_step
+ * (draco/runtime/cpu/executor.py:208-224, 273-277, 308-329).
+ */
+int draco_gguf_gemv_residual(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype, float* resid,
+                             void* resid_bf16, int64_t m, int64_t n, int64_t k, void* stream);
+
+/*
  * Prefill GEMM with the dequantization fused in (weight tiles decoded into
  * LDS, bf16 MFMA, float32 accumulate and output):
  *   y[m, n] = x_bf16[m, k] . W[n, k]^T (+ bias[n]),  m >= 1.

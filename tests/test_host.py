@@ -85,6 +85,19 @@ def test_error_codes_before_launch():
     trunc[4] = 100
     assert moe(*trunc) == _native.DRACO_EINVAL_SHAPE
     assert lib.draco_gguf_moe_workspace_size(64, 4096, 14336, 8, 2) > 64 * 2 * (4096 + 14336) * 4
+    # fused decode launches
+    w2 = (ctypes.c_void_p * 5)(*([FAKE] * 5))
+    nb = (ctypes.c_size_t * 5)(*([1 << 20] * 5))
+    nn = (ctypes.c_int64 * 5)(*([16] * 5))
+    ys = (ctypes.c_void_p * 5)(*([FAKE + 0x100000] * 5))
+    assert lib.draco_gguf_gemv_multi(12, 5, w2, nb, nn, ys, None, FAKE, 1, 1, 256, None) == _native.DRACO_EINVAL_ARG
+    assert lib.draco_gguf_gemv_multi(12, 2, w2, nb, nn, None, None, FAKE, 1, 1, 256, None) == _native.DRACO_EINVAL_ARG
+    assert lib.draco_gguf_gemv_swiglu(12, FAKE, FAKE, 1 << 20, FAKE, 1, None, None, 1, 16, 256, None) \
+        == _native.DRACO_EINVAL_ARG
+    # x overlapping the residual it updates
+    assert lib.draco_gguf_gemv_residual(12, FAKE, 1 << 20, FAKE + 0x1000, 0, FAKE + 0x1000, None, 1, 16, 256,
+                                        None) == _native.DRACO_EINVAL_ARG
+    assert "overlap" in _native.last_error()
 
 
 def test_check_maps_codes_to_reference_exceptions():

@@ -43,18 +43,31 @@ def log(*a):
 
 
 def time_launches(fns, reps):
-    """Average ms per launch of back-to-back launches on the current stream (HIP events)."""
+    """Average ms per launch of the launches in ``fns``, captured once into a
+    HIP graph and replayed ``reps`` times back to back; HIP events are recorded
+    on the stream the replays (and so the kernels) run on."""
     import torch
 
     for f in fns:
         f()
     torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in fns:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for f in fns:
+            f()
+    graph.replay()
+    torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for _ in range(reps):
-        for f in fns:
-            f()
+        graph.replay()
     end.record(stream)
     end.synchronize()
     return start.elapsed_time(end) / (reps * len(fns))
@@ -78,7 +91,7 @@ def dominant_kernel_roofline(ls, reps):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
     return {
-        "kernel": "gemv_kernel<Q4_K, M=1, bf16 x> on 14336x4096",
+        "kernel": "gemv_x1_kernel<Q4_K> (decode GEMV, M = 1, bf16 x) on a 14336 x 4096 Q4_K weight",
         "bound": "hbm",
         "achieved": round(achieved, 1),
         "peak": PEAK_HBM_GBS,
@@ -88,6 +101,7 @@ def dominant_kernel_roofline(ls, reps):
         "alg_bytes_per_launch": alg_bytes,
         "avg_launch_us": round(ms * 1e3, 3),
         "launches_timed": reps * len(fns),
+        "rotation": f"{len(mats)} distinct weights, {len(mats) * mats[0].nbytes / 1e9:.2f} GB (> 256 MB Infinity Cache)",
     }
 
 
@@ -112,36 +126,49 @@ def cpu_baseline(ls, step_bytes):
         b, t, shp = spec
         return gguf_ref.dequantize_matrix(t, b, shp)
 
+    def timed(fn, budget_s):
+        """Mean seconds per call of fn, repeated until budget_s has passed (at least twice)."""
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if n >= 2 and el >= budget_s:
+                return el / n
+
     with threadpool_limits(limits=cores):
         t0 = time.perf_counter()
         wl = {p: dq(spec) for p, spec in layer.items()}
-        wlm = dq(lm_part)
-        t_dequant = time.perf_counter() - t0
-        reps = 3
+        t_dq_layer = time.perf_counter() - t0
         t0 = time.perf_counter()
-        for _ in range(reps):
+        wlm = dq(lm_part)
+        t_dq_lm = time.perf_counter() - t0
+
+        def layer_fn():
             for p, w in wl.items():
                 matmul_ref.cpu_linear_f32(xi if p == "down" else x, w)
-            matmul_ref.cpu_linear_f32(x, wlm)
-        t_warm = (time.perf_counter() - t0) / reps
-    # scale: 32 layers and the full lm_head from 1 layer + 1/8 of the lm_head
-    layer_frac = sum(w.size for w in wl.values()) / (sum(w.size for w in wl.values()) + wlm.size)
-    t_layer, t_lm = t_warm * layer_frac, t_warm * (1 - layer_frac)
+
+        t_layer = timed(layer_fn, 6.0)
+        t_lm = timed(lambda: matmul_ref.cpu_linear_f32(x, wlm), 3.0)
+    # one step = 32 layers + the full lm_head (8 x the timed 1/8 of its rows)
     step_warm = ls.shape.n_layers * t_layer + 8 * t_lm
-    step_cold = step_warm + ls.shape.n_layers * t_dequant * layer_frac + 8 * t_dequant * (1 - layer_frac)
+    step_cold = step_warm + ls.shape.n_layers * t_dq_layer + 8 * t_dq_lm
     return {
         "value": round(step_bytes / step_warm / 1e9, 2),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
         "sample": (
-            "numpy restatement of the reference _dequantize + float32 x @ W.T on 1 decoder layer "
-            "(7 projections) + 1/8 of the lm_head rows, M = 1, warm fp32-weight cache (3 reps), "
-            f"scaled to {ls.shape.n_layers} layers + full lm_head (linear in weight count)"
+            "numpy restatement of the reference _dequantize + float32 x @ W.T (OpenBLAS, threads pinned to "
+            f"{cores}) on 1 decoder layer (7 projections) and 1/8 of the lm_head rows, M = 1, warm fp32-weight "
+            f"cache, each timed for >= 3-6 s; step = {ls.shape.n_layers} x layer + 8 x lm_head part"
         ),
+        "ms_per_step_warm": round(step_warm * 1e3, 2),
         "tokens_per_s_warm": round(1.0 / step_warm, 3),
         "tokens_per_s_cold": round(1.0 / step_cold, 4),
-        "sample_seconds": round(t_dequant + reps * t_warm, 2),
+        "dequant_s_layer": round(t_dq_layer, 3),
+        "dequant_s_lm_part": round(t_dq_lm, 3),
     }
 
 

@@ -3,7 +3,7 @@
 // Replaces _dequantize + x.astype(f32) @ W.T (draco/format/gguf.py:820-834,
 // draco/runtime/cpu/kernels/generic.py:32-33) per _linear call
 // (draco/runtime/cpu/executor.py:47-79), and _qkv (:243-271) for the fused form.
-#include "gemv_stream.h"
+#include "gemv_x1.h"
 
 namespace draco {
 
@@ -24,7 +24,7 @@ int gemv_multi_dispatch(int qtype, bool d_last, int n_mats, const void* const* w
   job.m = m;
   job.x = x;
   job.bias = bias;
-  return stream_dispatch<kPlain>(qtype, d_last, job, xbf16, s);
+  return gemv_dispatch_mode<kPlain>(qtype, d_last, job, xbf16, s);
 }
 
 int gemv_dispatch(int qtype, bool d_last, const void* w, const void* x, bool x_bf16, const float* bias, float* y,

@@ -244,21 +244,44 @@ __device__ __forceinline__ int perm_natural_pos(int l, int j) {
   return group_pos<QT>(l, e / GL) + (e % GL);
 }
 
+// Slot (j * 64 + l) of the permuted layout that holds natural chunk c of a
+// step (elements CE * c .. CE * c + CE - 1): the inverse of perm_natural_pos.
+template <int QT, bool XBF16>
+__device__ __forceinline__ int perm_slot_of_chunk(int c) {
+  constexpr int CE = XChunk<XBF16>::CE;
+  const int p = c * CE;  // natural element offset within the 2048-element step
+  int l, e;              // unit (= lane) and element index within the unit's G * GL activations
+  if constexpr (QT == kQ4_K) {
+    const int q = p & 255;
+    l = 8 * (p >> 8) + 2 * (q >> 6) + ((q >> 4) & 1);
+    e = 16 * ((q >> 5) & 1) + (q & 15);
+  } else if constexpr (QT == kQ6_K) {
+    const int q = p & 255;
+    l = 8 * (p >> 8) + 4 * (q >> 7) + ((q >> 3) & 3);
+    e = 8 * ((q >> 5) & 3) + (q & 7);
+  } else {
+    l = p >> 5;
+    e = p & 31;
+  }
+  return (e / CE) * 64 + l;
+}
+
+// Stages activation rows 0..m-1 (rows m..MT-1 zero) into LDS in the
+// permuted layout.  The global reads are contiguous (thread t reads chunk t,
+// so a wave's load instruction covers 1 KB of consecutive bytes); only the
+// LDS writes are scattered.  All threads of the workgroup must call it (it
+// ends in a barrier).
 template <int QT, int MT, bool XBF16, class XRow>
 __device__ __forceinline__ void stage_x_lds_perm(uint4* lds, int m, int k, XRow xrow) {
-  constexpr int CE = XChunk<XBF16>::CE, XB = XBF16 ? 2 : 4;
-  constexpr int JPS = 32 / CE;  // chunks per lane per step
-  const int chunks = k / CE;    // per activation row
+  constexpr int CE = XChunk<XBF16>::CE;
+  constexpr int CPS = 2048 / CE;  // chunks per step
+  const int chunks = k / CE;      // per activation row
   for (int i = threadIdx.x; i < MT * chunks; i += blockDim.x) {
     const int mi = i / chunks, c = i - mi * chunks;
-    const int step = c / (64 * JPS), q = c - step * 64 * JPS;
-    const int j = q >> 6, l = q & 63;
+    const int step = c / CPS, cs = c - step * CPS;
     uint4 v = {0u, 0u, 0u, 0u};
-    if (mi < m) {
-      const int p = step * 2048 + perm_natural_pos<QT, XBF16>(l, j);
-      v = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(xrow(mi)) + (size_t)p * XB);
-    }
-    lds[i] = v;
+    if (mi < m) v = reinterpret_cast<const uint4*>(xrow(mi))[c];
+    lds[(size_t)mi * chunks + (size_t)step * CPS + perm_slot_of_chunk<QT, XBF16>(cs)] = v;
   }
   __syncthreads();
 }

@@ -2,7 +2,7 @@
 // optional bfloat16 copy of the updated residual for the next projection.
 // Replaces _o_proj / the down projection plus the residual adds of
 // forward_step (draco/runtime/cpu/executor.py:273-277, 308-329).
-#include "gemv_stream.h"
+#include "gemv_x1.h"
 
 namespace draco {
 
@@ -19,7 +19,7 @@ int gemv_resid_dispatch(int qtype, bool d_last, const void* w, const void* x, bo
   job.x = x;
   job.resid = resid;
   job.resid_bf16 = resid_bf16;
-  return stream_dispatch<kResid>(qtype, d_last, job, xbf16, s);
+  return gemv_dispatch_mode<kResid>(qtype, d_last, job, xbf16, s);
 }
 
 }  // namespace draco

@@ -1,7 +1,7 @@
 // Fused gate/up GEMV with the SwiGLU epilogue: y = silu(W_gate x) * (W_up x).
 // Replaces the reference executor's _mlp gate/up projections and swiglu
 // (draco/runtime/cpu/executor.py:208-224, draco/runtime/cpu/ops.py:19-27).
-#include "gemv_stream.h"
+#include "gemv_x1.h"
 
 namespace draco {
 
@@ -19,7 +19,7 @@ int gemv_swiglu_dispatch(int qtype, bool d_last, const void* w_gate, const void*
   job.k = k;
   job.m = m;
   job.x = x;
-  return stream_dispatch<kSwiGLU>(qtype, d_last, job, xbf16, s);
+  return gemv_dispatch_mode<kSwiGLU>(qtype, d_last, job, xbf16, s);
 }
 
 }  // namespace draco

@@ -1,0 +1,311 @@
+// Single-token decode GEMV (M = 1, bfloat16 activations) for the K-quants,
+// the shape of every projection of a batch-1 decode step.
+//
+// Each lane decodes 64-weight units: a Q4_K unit is a quarter super-block
+// (32 qs bytes = sub-blocks 2j and 2j + 1, one scale and min each), a Q6_K
+// unit is a quarter super-block too (16 l values of one half, all four t
+// rows, one int8 scale per t).  The per-unit fields are fetched with one
+// vector load each: Q4_K's are 16-byte aligned; Q6_K's sit at even offsets
+// (210-byte blocks) and use the unaligned dwordx4 / dwordx2 loads that the
+// gfx9 HSA memory model allows, so a 64-weight Q6_K unit costs five load
+// instructions instead of thirteen dword loads.
+//
+// Lane l of a wave owns unit l, l + 64, ... of every row the wave computes
+// ("step" s covers units 64 s .. 64 s + 63), so the activations a lane needs
+// are the same for all of its rows: the wave loads them into registers once
+// per step (64 bfloat16 = 32 VGPRs), sums them per group, and reuses them for
+// its R rows.  No LDS and no workgroup barriers: a wave issues the loads of a
+// step for all R rows right after the activation loads and starts
+// multiplying as soon as its first row has landed.
+//
+// Codes are turned into exact bfloat16 pairs (128 + code, one v_perm_b32 per
+// pair) and multiplied with v_dot2_f32_bf16; scale and min are applied once
+// per 32- (Q4_K) or 16-weight (Q6_K) group:
+//   Q4_K  sum_i w_i x_i = a * (dot - 128 xs) + b * xs,   a = d sc, b = -dmin m
+//   Q6_K  sum_i w_i x_i = a * (dot - 160 xs),            a = d sc  (codes - 32)
+// with dot = sum (128 + code_i) x_i and xs = sum x_i over the group.
+// Launch modes and epilogues as in gemv_stream.h (kPlain with up to 4
+// matrices sharing x, kSwiGLU, kResid).
+#pragma once
+
+#include "gemv_stream.h"
+
+namespace draco {
+
+template <int QT> struct X1Fmt;
+template <> struct X1Fmt<kQ4_K> { static constexpr int UPB = 4, G = 2, GL = 32; };
+template <> struct X1Fmt<kQ6_K> { static constexpr int UPB = 4, G = 4, GL = 16; };
+
+template <int QT> struct X1Raw;
+template <> struct X1Raw<kQ4_K> { uint4 head, qs0, qs1; };
+template <> struct X1Raw<kQ6_K> { uint4 qla, qlb, qh; uint32_t sc0, sc1, d; };
+
+typedef int x1_v4i __attribute__((ext_vector_type(4)));
+typedef int x1_v2i __attribute__((ext_vector_type(2)));
+
+struct X1Buf {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int soff;  // wave-uniform byte offset of the row
+  __device__ __forceinline__ uint4 b128(int off) const {
+    const x1_v4i v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, soff, 0);
+    return uint4{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+  }
+  __device__ __forceinline__ void b64(int off, uint32_t& lo, uint32_t& hi) const {
+    const x1_v2i v = __builtin_amdgcn_raw_buffer_load_b64(rsrc, off, soff, 0);
+    lo = (uint32_t)v.x;
+    hi = (uint32_t)v.y;
+  }
+  __device__ __forceinline__ uint32_t b16(int off) const {
+    return (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rsrc, off, soff, 0);
+  }
+};
+
+// Unit u (64 weights) of a row; offsets relative to the row start.
+template <int QT, bool DL>
+__device__ __forceinline__ X1Raw<QT> x1_load(const X1Buf& b, int u) {
+  X1Raw<QT> r;
+  const int blk = (u >> 2) * Fmt<QT>::BYTES, j = u & 3;
+  if constexpr (QT == kQ4_K) {
+    r.head = b.b128(blk);
+    r.qs0 = b.b128(blk + 16 + 32 * j);
+    r.qs1 = b.b128(blk + 32 + 32 * j);
+  } else {
+    constexpr int QL = DL ? 0 : 2, QH = DL ? 128 : 130, SC = DL ? 192 : 194, D = DL ? 208 : 0;
+    const int n = j >> 1, h = j & 1;
+    r.qla = b.b128(blk + QL + 64 * n + 16 * h);
+    r.qlb = b.b128(blk + QL + 64 * n + 32 + 16 * h);
+    r.qh = b.b128(blk + QH + 32 * n + 16 * h);
+    b.b64(blk + SC + 8 * n, r.sc0, r.sc1);
+    r.d = b.b16(blk + D);
+  }
+  return r;
+}
+
+// Element offset (within the row) of group g of unit u.
+template <int QT>
+__device__ __forceinline__ int x1_group_pos(int u, int g) {
+  const int j = u & 3;
+  if constexpr (QT == kQ4_K) return 256 * (u >> 2) + 64 * j + 32 * g;
+  return 256 * (u >> 2) + 128 * (j >> 1) + 32 * g + 16 * (j & 1);
+}
+
+// The lane's activations for unit u: G groups of GL bf16 = 8 x 16 bytes.
+struct X1Act {
+  uint32_t w[32];
+  float xs[4];
+};
+
+template <int QT, bool FULL>
+__device__ __forceinline__ void x1_load_x(const uint16_t* __restrict__ x, int u, bool live, X1Act& a) {
+  constexpr int G = X1Fmt<QT>::G, GL = X1Fmt<QT>::GL, CPG = GL / 8;  // 16-byte chunks per group
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint4* p = reinterpret_cast<const uint4*>(x + x1_group_pos<QT>(u, g));
+#pragma unroll
+    for (int c = 0; c < CPG; ++c) {
+      uint4 v = p[c];
+      if constexpr (!FULL) {
+        if (!live) v = uint4{0u, 0u, 0u, 0u};
+      }
+      a.w[(g * CPG + c) * 4 + 0] = v.x;
+      a.w[(g * CPG + c) * 4 + 1] = v.y;
+      a.w[(g * CPG + c) * 4 + 2] = v.z;
+      a.w[(g * CPG + c) * 4 + 3] = v.w;
+    }
+  }
+}
+
+template <int QT>
+__device__ __forceinline__ void x1_group_sums(X1Act& a) {
+  constexpr int G = X1Fmt<QT>::G, GL = X1Fmt<QT>::GL;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float t = 0.f;
+#pragma unroll
+    for (int j = 0; j < GL / 2; ++j) t = dot2bf(a.w[g * (GL / 2) + j], kOnePair, t);
+    a.xs[g] = t;
+  }
+}
+
+// Per-lane constants of the unit position j = u & 3 (the same for every step
+// of a lane, since a step is 64 units): Q4_K sub-block half and byte shift,
+// Q6_K half-row h.
+struct X1Lane {
+  uint32_t hi_mask;  // Q4_K: all ones when the unit's sub-blocks are 4..7
+  uint32_t sh;       // Q4_K: 16 * (j & 1), byte offset of sub-block 2j in the scale word; Q6_K: 8 * (j & 1)
+};
+
+template <int QT>
+__device__ __forceinline__ X1Lane x1_lane(int lane) {
+  const int j = lane & 3;
+  X1Lane c;
+  c.hi_mask = j >= 2 ? 0xFFFFFFFFu : 0u;
+  c.sh = QT == kQ4_K ? 16u * (j & 1) : 8u * (j & 1);
+  return c;
+}
+
+// sum_i w_i x_i over the unit.
+template <int QT>
+__device__ __forceinline__ float x1_unit_dot(const X1Raw<QT>& r, const X1Lane& c, const X1Act& a) {
+  if constexpr (QT == kQ4_K) {
+    const float d = f16_bits_to_f32(r.head.x), dmin = f16_bits_to_f32(r.head.x >> 16);
+    // 6-bit scales / mins of sub-blocks 2j, 2j + 1 (the reference's _scale_min
+    // in SWAR form: byte i of scw / mw belongs to sub-block i, or 4 + i when
+    // the unit is in the upper half), selected without branches
+    const uint32_t s0 = r.head.y, s1 = r.head.z, s2 = r.head.w;
+    const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, m_lo = s1 & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+    const uint32_t scw = ((sc_hi & c.hi_mask) | (sc_lo & ~c.hi_mask)) >> c.sh;
+    const uint32_t mw = ((m_hi & c.hi_mask) | (m_lo & ~c.hi_mask)) >> c.sh;
+    const uint32_t q[8] = {r.qs0.x, r.qs0.y, r.qs0.z, r.qs0.w, r.qs1.x, r.qs1.y, r.qs1.z, r.qs1.w};
+    float out = 0.f;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      float dot = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t cw = g == 0 ? nib_lo(q[i]) : nib_hi(q[i]);
+        dot = dot2bf(code_pair_lo(cw), a.w[16 * g + 2 * i], dot);
+        dot = dot2bf(code_pair_hi(cw), a.w[16 * g + 2 * i + 1], dot);
+      }
+      const float av = d * ubyte_f(scw, g);
+      // a * (dot - 128 xs) - dmin * m * xs
+      out = fmaf(av, fmaf(-kCodeBias, a.xs[g], dot), out);
+      out = fmaf(-(dmin * ubyte_f(mw, g)), a.xs[g], out);
+    }
+    return out;
+  } else {
+    const float d = f16_bits_to_f32(r.d);
+    const uint32_t ql[2][4] = {{r.qla.x, r.qla.y, r.qla.z, r.qla.w}, {r.qlb.x, r.qlb.y, r.qlb.z, r.qlb.w}};
+    const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+    // scale of row t: sc[8n + h + 2t] = byte 2t of the 8 scale bytes shifted by h
+    const uint32_t sa = r.sc0 >> c.sh, sb = r.sc1 >> c.sh;
+    float out = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float dot = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t cw = q6_codes(t, ql[0][i], ql[1][i], qh[i]);
+        dot = dot2bf(code_pair_lo(cw), a.w[8 * t + 2 * i], dot);
+        dot = dot2bf(code_pair_hi(cw), a.w[8 * t + 2 * i + 1], dot);
+      }
+      const float sc = sbyte_f(t < 2 ? sa : sb, 2 * (t & 1));
+      out = fmaf(d * sc, fmaf(-(kCodeBias + 32.f), a.xs[t], dot), out);
+    }
+    return out;
+  }
+}
+
+template <int QT, bool DL, int MODE, int R, bool FULL, int OCC>
+__global__ __launch_bounds__(256, OCC) void gemv_x1_kernel(StreamJob job) {
+  constexpr int NR = MODE == kSwiGLU ? 2 : 1;
+  constexpr int RR = R * NR;
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
+  if (row0 >= job.rows) return;
+  const int units = job.k >> 6;
+  const int steps = (units + 63) >> 6;
+  const uint16_t* x = static_cast<const uint16_t*>(job.x);
+
+  // buffer resource per matrix, row offsets in the scalar offset
+  X1Buf rb[RR];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int grow = min(row0 + r, job.rows - 1);
+    int mat = 0, lrow = grow;
+    if constexpr (MODE == kPlain) row_of(job, grow, mat, lrow);
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+      const int m = NR == 2 ? q : mat;
+      rb[r * NR + q].rsrc = make_rsrc(job.w[m], (uint32_t)((int64_t)job.n[m] * job.row_bytes));
+      rb[r * NR + q].soff = (int)((int64_t)lrow * job.row_bytes);
+    }
+  }
+
+  const X1Lane lc = x1_lane<QT>(lane);
+  float acc[RR];
+#pragma unroll
+  for (int i = 0; i < RR; ++i) acc[i] = 0.f;
+
+  for (int s = 0; s < steps; ++s) {
+    const int u = lane + 64 * s;
+    const bool live = FULL || u < units;
+    const int ul = live ? u : units - 1;  // lanes past the row end re-read the last unit, x = 0
+    X1Act xa;
+    x1_load_x<QT, FULL>(x, ul, live, xa);
+    X1Raw<QT> raw[RR];
+#pragma unroll
+    for (int i = 0; i < RR; ++i) raw[i] = x1_load<QT, DL>(rb[i], ul);
+    x1_group_sums<QT>(xa);
+#pragma unroll
+    for (int i = 0; i < RR; ++i) acc[i] += x1_unit_dot<QT>(raw[i], lc, xa);
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int grow = row0 + r;
+    int mat = 0, lrow = grow;
+    if constexpr (MODE == kPlain) row_of(job, grow < job.rows ? grow : job.rows - 1, mat, lrow);
+    float v[NR];
+#pragma unroll
+    for (int q = 0; q < NR; ++q) v[q] = wave_sum_dpp(acc[r * NR + q]);
+    if (lane != r || grow >= job.rows) continue;
+    const size_t o = (size_t)lrow;
+    if constexpr (MODE == kResid) {
+      const float out = job.resid[o] + v[0];
+      job.resid[o] = out;
+      if (job.resid_bf16) job.resid_bf16[o] = f32_to_bf16_rne(out);
+    } else {
+      float out = v[0];
+      if constexpr (MODE == kSwiGLU) out = silu(v[0]) * v[1];
+      if (MODE == kPlain && job.bias) out += job.bias[lrow];
+      if (job.y[mat]) job.y[mat][o] = out;
+      if (job.yb[mat]) job.yb[mat][o] = f32_to_bf16_rne(out);
+    }
+  }
+}
+
+template <int QT, bool DL, int MODE, int R, int OCC = 1, bool ALLOW_FULL = true>
+static int launch_x1(const StreamJob& job, hipStream_t s) {
+  const int waves = (job.rows + R - 1) / R;
+  const int blocks = (waves + 3) / 4;
+  if (ALLOW_FULL && (job.k >> 6) % 64 == 0)
+    hipLaunchKernelGGL((gemv_x1_kernel<QT, DL, MODE, R, true, OCC>), dim3(blocks), dim3(256), 0, s, job);
+  else
+    hipLaunchKernelGGL((gemv_x1_kernel<QT, DL, MODE, R, false, OCC>), dim3(blocks), dim3(256), 0, s, job);
+  return check_launch("gemv_x1");
+}
+
+}  // namespace draco
+
+namespace draco {
+
+// Decode GEMV dispatch: single-token bfloat16 launches of the K-quants go to
+// the 64-weight-unit kernel above; everything else (Q8_0 / Q4_0, float32
+// activations, 2..16 activation rows) to the streaming kernel.  The x1 code
+// is compiled with predicated activation loads (ALLOW_FULL = false): letting
+// the compiler interleave each row's loads with the previous row's math was
+// measured faster than hoisting every load of the step.
+template <int MODE>
+static int gemv_dispatch_mode(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s) {
+  // (kSwiGLU multiplies two weight rows per output row; the streaming kernel
+  // was measured faster for it)
+  if constexpr (MODE != kSwiGLU) {
+    bool x1 = job.m == 1 && xbf16 && (qtype == kQ4_K || qtype == kQ6_K);
+    for (int i = 0; i < job.n_mats; ++i)
+      if ((int64_t)job.n[i] * job.row_bytes >= ((int64_t)1 << 31)) x1 = false;  // 32-bit buffer offsets
+    if (x1) {
+      if (qtype == kQ4_K) return launch_x1<kQ4_K, false, MODE, 2, 1, false>(job, s);
+      if (job.rows >= 32768)
+        return d_last ? launch_x1<kQ6_K, true, MODE, 4, 1, false>(job, s)
+                      : launch_x1<kQ6_K, false, MODE, 4, 1, false>(job, s);
+      return d_last ? launch_x1<kQ6_K, true, MODE, 2, 1, false>(job, s)
+                    : launch_x1<kQ6_K, false, MODE, 2, 1, false>(job, s);
+    }
+  }
+  return stream_dispatch<MODE>(qtype, d_last, job, xbf16, s);
+}
+
+}  // namespace draco

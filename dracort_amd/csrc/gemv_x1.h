@@ -127,6 +127,75 @@ __device__ __forceinline__ void x1_group_sums(X1Act& a) {
   }
 }
 
+// LDS image of the activations (XL kernels): for each step s (64 units of 64
+// weights) 512 16-byte chunks in lane-permuted order -- chunk j of the
+// activations of unit l at slot s * 512 + j * 64 + l, so the eight
+// ds_read_b128 of a lane's unit are each 1 KB contiguous across the wave --
+// followed by the per-group sums, float [step][g][64].
+template <int QT>
+__device__ __forceinline__ int x1_slot_of_chunk(int c) {  // natural chunk (8 bf16) within a step
+  const int p = c * 8;
+  if constexpr (QT == kQ4_K) return ((p & 63) >> 3) * 64 + (p >> 6);
+  const int q = p & 255;
+  const int u = 4 * (p >> 8) + 2 * (q >> 7) + ((q >> 4) & 1);
+  const int j = 2 * ((q >> 5) & 3) + ((q >> 3) & 1);
+  return j * 64 + u;
+}
+
+inline size_t x1_lds_bytes(int qtype, int k) {
+  const int steps = ((k >> 6) + 63) >> 6;
+  const int g = qtype == kQ4_K ? 2 : 4;
+  return (size_t)steps * 512 * 16 + (size_t)steps * g * 64 * 4;
+}
+
+// Every thread of the workgroup calls this; it ends in a barrier.
+template <int QT>
+__device__ __forceinline__ void x1_stage(uint4* lds, const uint16_t* __restrict__ x, int k) {
+  constexpr int G = X1Fmt<QT>::G, CPG = X1Fmt<QT>::GL / 8;
+  const int units = k >> 6, steps = (units + 63) >> 6;
+  const int chunks = k >> 3;
+  const uint4* xs = reinterpret_cast<const uint4*>(x);
+  for (int c = threadIdx.x; c < chunks; c += blockDim.x)
+    lds[(c >> 9) * 512 + x1_slot_of_chunk<QT>(c & 511)] = xs[c];
+  __syncthreads();
+  float* sums = reinterpret_cast<float*>(lds + steps * 512);
+  for (int i = threadIdx.x; i < units * G; i += blockDim.x) {
+    const int u = i / G, g = i - u * G;
+    const int st = u >> 6, l = u & 63;
+    float t = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < CPG; ++cc) {
+      const uint4 v = lds[st * 512 + (g * CPG + cc) * 64 + l];
+      t = dot2bf(v.x, kOnePair, t);
+      t = dot2bf(v.y, kOnePair, t);
+      t = dot2bf(v.z, kOnePair, t);
+      t = dot2bf(v.w, kOnePair, t);
+    }
+    sums[(st * G + g) * 64 + l] = t;
+  }
+  __syncthreads();
+}
+
+// The lane's activations of step s from the LDS image (zero when !live).
+template <int QT>
+__device__ __forceinline__ void x1_read_lds(const uint4* __restrict__ lds, int k, int s, int lane, bool live,
+                                            X1Act& a) {
+  constexpr int G = X1Fmt<QT>::G;
+  const int steps = ((k >> 6) + 63) >> 6;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    uint4 v = lds[s * 512 + j * 64 + lane];
+    if (!live) v = uint4{0u, 0u, 0u, 0u};
+    a.w[4 * j + 0] = v.x;
+    a.w[4 * j + 1] = v.y;
+    a.w[4 * j + 2] = v.z;
+    a.w[4 * j + 3] = v.w;
+  }
+  const float* sums = reinterpret_cast<const float*>(lds + steps * 512);
+#pragma unroll
+  for (int g = 0; g < G; ++g) a.xs[g] = live ? sums[(s * G + g) * 64 + lane] : 0.f;
+}
+
 // Per-lane constants of the unit position j = u & 3 (the same for every step
 // of a lane, since a step is 64 units): Q4_K sub-block half and byte shift,
 // Q6_K half-row h.
@@ -198,12 +267,14 @@ __device__ __forceinline__ float x1_unit_dot(const X1Raw<QT>& r, const X1Lane& c
   }
 }
 
-template <int QT, bool DL, int MODE, int R, bool FULL, int OCC>
+template <int QT, bool DL, int MODE, int R, bool FULL, int OCC, bool XL>
 __global__ __launch_bounds__(256, OCC) void gemv_x1_kernel(StreamJob job) {
   constexpr int NR = MODE == kSwiGLU ? 2 : 1;
   constexpr int RR = R * NR;
+  extern __shared__ uint4 x1_smem[];
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
+  if constexpr (XL) x1_stage<QT>(x1_smem, static_cast<const uint16_t*>(job.x), job.k);
   if (row0 >= job.rows) return;
   const int units = job.k >> 6;
   const int steps = (units + 63) >> 6;
@@ -233,12 +304,18 @@ __global__ __launch_bounds__(256, OCC) void gemv_x1_kernel(StreamJob job) {
     const int u = lane + 64 * s;
     const bool live = FULL || u < units;
     const int ul = live ? u : units - 1;  // lanes past the row end re-read the last unit, x = 0
-    X1Act xa;
-    x1_load_x<QT, FULL>(x, ul, live, xa);
     X1Raw<QT> raw[RR];
+    X1Act xa;
+    if constexpr (XL) {
 #pragma unroll
-    for (int i = 0; i < RR; ++i) raw[i] = x1_load<QT, DL>(rb[i], ul);
-    x1_group_sums<QT>(xa);
+      for (int i = 0; i < RR; ++i) raw[i] = x1_load<QT, DL>(rb[i], ul);
+      x1_read_lds<QT>(x1_smem, job.k, s, lane, live, xa);
+    } else {
+      x1_load_x<QT, FULL>(x, ul, live, xa);
+#pragma unroll
+      for (int i = 0; i < RR; ++i) raw[i] = x1_load<QT, DL>(rb[i], ul);
+      x1_group_sums<QT>(xa);
+    }
 #pragma unroll
     for (int i = 0; i < RR; ++i) acc[i] += x1_unit_dot<QT>(raw[i], lc, xa);
   }
@@ -267,14 +344,97 @@ __global__ __launch_bounds__(256, OCC) void gemv_x1_kernel(StreamJob job) {
   }
 }
 
-template <int QT, bool DL, int MODE, int R, int OCC = 1, bool ALLOW_FULL = true>
+// Persistent form for rows of one step (K <= 4096): a fixed grid of waves,
+// wave w computes rows w, w + W, w + 2W, ... (W = all waves) with the packed
+// bytes of the next PF rows in flight while it multiplies the current one, so
+// the loads are issued at the pace the math consumes them (instead of every
+// wave requesting its rows at once and all of them finishing together).  The
+// activations (the bf16 LDS image) are read into registers once.
+template <int QT, bool DL, int MODE, int PF>
+__global__ __launch_bounds__(256) void gemv_x1p_kernel(StreamJob job) {
+  constexpr int NR = MODE == kSwiGLU ? 2 : 1;
+  extern __shared__ uint4 x1_smem[];
+  const int lane = threadIdx.x & 63;
+  const int W = gridDim.x * 4;
+  const int w = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  x1_stage<QT>(x1_smem, static_cast<const uint16_t*>(job.x), job.k);
+  const int nrow = job.rows > w ? (job.rows - w + W - 1) / W : 0;
+  if (nrow == 0) return;
+  const int units = job.k >> 6;
+  const bool live = lane < units;
+  const int ul = live ? lane : units - 1;
+  const X1Lane lc = x1_lane<QT>(lane);
+  X1Act xa;
+  x1_read_lds<QT>(x1_smem, job.k, 0, lane, live, xa);
+
+  auto rowbuf = [&](int i, int q) {
+    int mat = 0, lrow = w + i * W;
+    if constexpr (MODE == kPlain) row_of(job, lrow, mat, lrow);
+    const int m = NR == 2 ? q : mat;
+    X1Buf b;
+    b.rsrc = make_rsrc(job.w[m], (uint32_t)((int64_t)job.n[m] * job.row_bytes));
+    b.soff = (int)((int64_t)lrow * job.row_bytes);
+    return b;
+  };
+  X1Raw<QT> buf[PF][NR];
+#pragma unroll
+  for (int p = 0; p < PF; ++p)
+#pragma unroll
+    for (int q = 0; q < NR; ++q) buf[p][q] = x1_load<QT, DL>(rowbuf(min(p, nrow - 1), q), ul);
+
+  for (int i0 = 0; i0 < nrow; i0 += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      const int i = i0 + p;
+      if (i < nrow) {
+        float v[NR];
+#pragma unroll
+        for (int q = 0; q < NR; ++q) {
+          v[q] = wave_sum_dpp(x1_unit_dot<QT>(buf[p][q], lc, xa));
+        }
+        if (i + PF < nrow) {
+#pragma unroll
+          for (int q = 0; q < NR; ++q) buf[p][q] = x1_load<QT, DL>(rowbuf(i + PF, q), ul);
+        }
+        if (lane == 0) {
+          int mat = 0, lrow = w + i * W;
+          if constexpr (MODE == kPlain) row_of(job, lrow, mat, lrow);
+          if constexpr (MODE == kResid) {
+            const float out = job.resid[lrow] + v[0];
+            job.resid[lrow] = out;
+            if (job.resid_bf16) job.resid_bf16[lrow] = f32_to_bf16_rne(out);
+          } else {
+            float out = v[0];
+            if constexpr (MODE == kSwiGLU) out = silu(v[0]) * v[1];
+            if (MODE == kPlain && job.bias) out += job.bias[lrow];
+            if (job.y[mat]) job.y[mat][lrow] = out;
+            if (job.yb[mat]) job.yb[mat][lrow] = f32_to_bf16_rne(out);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int QT, bool DL, int MODE, int PF>
+static int launch_x1p(const StreamJob& job, int blocks_per_cu, hipStream_t s) {
+  const size_t lds = x1_lds_bytes(QT, job.k);
+  const int need = (job.rows + 3) / 4;
+  const int blocks = std::max(1, std::min(need, device_cus() * blocks_per_cu));
+  hipLaunchKernelGGL((gemv_x1p_kernel<QT, DL, MODE, PF>), dim3(blocks), dim3(256), lds, s, job);
+  return check_launch("gemv_x1p");
+}
+
+template <int QT, bool DL, int MODE, int R, int OCC = 1, bool ALLOW_FULL = true, bool XL = false>
 static int launch_x1(const StreamJob& job, hipStream_t s) {
   const int waves = (job.rows + R - 1) / R;
   const int blocks = (waves + 3) / 4;
+  const size_t lds = XL ? x1_lds_bytes(QT, job.k) : 0;
+  if (lds > 64 * 1024) return set_error(DRACO_EINVAL_SHAPE, "activation image needs %zu bytes of LDS", lds);
   if (ALLOW_FULL && (job.k >> 6) % 64 == 0)
-    hipLaunchKernelGGL((gemv_x1_kernel<QT, DL, MODE, R, true, OCC>), dim3(blocks), dim3(256), 0, s, job);
+    hipLaunchKernelGGL((gemv_x1_kernel<QT, DL, MODE, R, true, OCC, XL>), dim3(blocks), dim3(256), lds, s, job);
   else
-    hipLaunchKernelGGL((gemv_x1_kernel<QT, DL, MODE, R, false, OCC>), dim3(blocks), dim3(256), 0, s, job);
+    hipLaunchKernelGGL((gemv_x1_kernel<QT, DL, MODE, R, false, OCC, XL>), dim3(blocks), dim3(256), lds, s, job);
   return check_launch("gemv_x1");
 }
 
@@ -283,26 +443,29 @@ static int launch_x1(const StreamJob& job, hipStream_t s) {
 namespace draco {
 
 // Decode GEMV dispatch: single-token bfloat16 launches of the K-quants go to
-// the 64-weight-unit kernel above; everything else (Q8_0 / Q4_0, float32
-// activations, 2..16 activation rows) to the streaming kernel.  The x1 code
-// is compiled with predicated activation loads (ALLOW_FULL = false): letting
-// the compiler interleave each row's loads with the previous row's math was
+// the 64-weight-unit kernels above -- the persistent form when a row is one
+// step (K <= 4096), the one-shot form for longer rows (both with the LDS
+// activation image); everything else (Q8_0 / Q4_0, float32
+// activations, 2..16 activation rows) to the streaming kernel.  The one-shot
+// form is compiled with predicated loads (ALLOW_FULL = false): letting the
+// compiler interleave each row's loads with the previous row's math was
 // measured faster than hoisting every load of the step.
 template <int MODE>
 static int gemv_dispatch_mode(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s) {
-  // (kSwiGLU multiplies two weight rows per output row; the streaming kernel
-  // was measured faster for it)
+  bool x1 = job.m == 1 && xbf16 && (qtype == kQ4_K || qtype == kQ6_K);
+  for (int i = 0; i < job.n_mats; ++i)
+    if ((int64_t)job.n[i] * job.row_bytes >= ((int64_t)1 << 31)) x1 = false;  // 32-bit buffer offsets
+  if (x1 && job.k <= 4096) {
+    constexpr int kBlocksPerCu = 4;
+    if (qtype == kQ4_K) return launch_x1p<kQ4_K, false, MODE, 2>(job, kBlocksPerCu, s);
+    return d_last ? launch_x1p<kQ6_K, true, MODE, 2>(job, kBlocksPerCu, s)
+                  : launch_x1p<kQ6_K, false, MODE, 2>(job, kBlocksPerCu, s);
+  }
   if constexpr (MODE != kSwiGLU) {
-    bool x1 = job.m == 1 && xbf16 && (qtype == kQ4_K || qtype == kQ6_K);
-    for (int i = 0; i < job.n_mats; ++i)
-      if ((int64_t)job.n[i] * job.row_bytes >= ((int64_t)1 << 31)) x1 = false;  // 32-bit buffer offsets
-    if (x1) {
-      if (qtype == kQ4_K) return launch_x1<kQ4_K, false, MODE, 2, 1, false>(job, s);
-      if (job.rows >= 32768)
-        return d_last ? launch_x1<kQ6_K, true, MODE, 4, 1, false>(job, s)
-                      : launch_x1<kQ6_K, false, MODE, 4, 1, false>(job, s);
-      return d_last ? launch_x1<kQ6_K, true, MODE, 2, 1, false>(job, s)
-                    : launch_x1<kQ6_K, false, MODE, 2, 1, false>(job, s);
+    if (x1 && x1_lds_bytes(qtype, job.k) <= 64 * 1024) {
+      if (qtype == kQ4_K) return launch_x1<kQ4_K, false, MODE, 2, 1, false, true>(job, s);
+      return d_last ? launch_x1<kQ6_K, true, MODE, 2, 1, false, true>(job, s)
+                    : launch_x1<kQ6_K, false, MODE, 2, 1, false, true>(job, s);
     }
   }
   return stream_dispatch<MODE>(qtype, d_last, job, xbf16, s);

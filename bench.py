@@ -35,6 +35,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "Q4_K dequant-GEMV HBM GB/s (% of peak); 8B-shape decode tokens/s at 1 GPU"
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2516.6  # dense bf16 MFMA, 256 CU x 4096 FLOP/clk x 2.4 GHz
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_14336x4096_m1_traffic.json")
 
 
@@ -172,6 +173,98 @@ def cpu_baseline(ls, step_bytes):
     }
 
 
+def rotation(make, nbytes, min_total=1 << 30):
+    """Distinct copies of a synthetic weight so that a timed rotation streams
+    >= min_total bytes (beyond the 256 MB Infinity Cache)."""
+    import torch
+
+    first = make()
+    n = max(2, -(-min_total // nbytes))
+    return [first] + [torch.empty_like(first).copy_(first) for _ in range(n - 1)]
+
+
+def suite(reps: int):
+    """The other configurations of the path, one JSON line each (stdout)."""
+    import torch
+
+    from dracort_amd.format.gguf import tensor_bytes
+    from dracort_amd.kernels import gguf_gemm, gguf_gemv, gguf_moe, moe_workspace_bytes
+    from dracort_amd.runtime.decode import synthetic_weight
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    lines = []
+
+    def gemv_line(cfg, t, n, k, m, xdtype):
+        nb = tensor_bytes(t, (n, k))
+        mats = rotation(lambda: synthetic_weight(n, k, t, gen, "cuda").data, nb)
+        x = torch.randn((m, k), device="cuda").to(xdtype)
+        y = torch.empty((m, n), device="cuda")
+        ms = time_launches([lambda w=w: gguf_gemv(x, w, t, (n, k), out=y) for w in mats], reps)
+        alg = nb + x.numel() * x.element_size() + y.numel() * 4
+        del mats
+        return {"config": cfg, "kernel": "decode GEMV", "ggml_type": t, "shape": [n, k], "m": m,
+                "x_dtype": str(xdtype).replace("torch.", ""), "us_per_launch": round(ms * 1e3, 3),
+                "GB_s": round(alg / (ms * 1e-3) / 1e9, 1), "frac_hbm_peak": round(alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                "alg_bytes": alg}
+
+    # 1: Q8_0 GEMV 4096 x 4096, float32 activations
+    lines.append(gemv_line(1, 8, 4096, 4096, 1, torch.float32))
+    # 2: Q4_0 GEMV at the Llama-3-8B projection shapes, batch 1 / 4 / 8, float32 activations
+    for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
+        for m in (1, 4, 8):
+            lines.append(gemv_line(2, 2, n, k, m, torch.float32))
+    # 3 (single kernels): Q4_K / Q6_K GEMVs at M = 1 and 16, bf16 activations
+    for t, n, k in ((12, 14336, 4096), (12, 4096, 4096), (14, 4096, 14336), (14, 128256, 4096)):
+        for m in (1, 16):
+            lines.append(gemv_line(3, t, n, k, m, torch.bfloat16))
+    # 4: prefill GEMM, Q4_K weights, bf16 activations, M = 512 / 2048
+    for n, k in ((14336, 4096), (4096, 14336)):
+        w = synthetic_weight(n, k, 12, gen, "cuda")
+        for m in (512, 2048):
+            x = torch.randn((m, k), device="cuda").to(torch.bfloat16)
+            y = torch.empty((m, n), device="cuda")
+            ms = time_launches([lambda: gguf_gemm(x, w.data, 12, (n, k), out=y)], reps)
+            flops = 2.0 * m * n * k
+            lines.append({"config": 4, "kernel": "prefill GEMM (bf16 MFMA)", "ggml_type": 12, "shape": [n, k], "m": m,
+                          "us_per_launch": round(ms * 1e3, 2), "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1),
+                          "frac_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)})
+        del w
+    # 5: Mixtral-8x7B MoE FFN, Q4_K experts, 64 tokens, top-2
+    hid, inter, ne, tok = 4096, 14336, 8, 64
+    wg = [synthetic_weight(inter, hid, 12, gen, "cuda").data for _ in range(ne)]
+    wu = [synthetic_weight(inter, hid, 12, gen, "cuda").data for _ in range(ne)]
+    wd = [synthetic_weight(hid, inter, 12, gen, "cuda").data for _ in range(ne)]
+    x = torch.randn((tok, hid), device="cuda").to(torch.bfloat16)
+    logits = torch.randn((tok, ne), device="cuda")
+    ws = torch.empty(moe_workspace_bytes(tok, hid, inter, ne, 2), dtype=torch.uint8, device="cuda")
+    y = torch.empty((tok, hid), device="cuda")
+    ms = time_launches([lambda: gguf_moe(x, logits, wg, wu, wd, 12, inter, top_k=2, workspace=ws, out=y)], reps)
+    wbytes = sum(t.numel() for t in wg + wu + wd)
+    lines.append({"config": 5, "kernel": "MoE FFN (route + grouped expert GEMVs + combine)", "experts": ne, "tokens": tok,
+                  "top_k": 2, "us_per_call": round(ms * 1e3, 2), "weight_bytes": wbytes,
+                  "GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1), "frac_hbm_peak": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
+    return lines
+
+
+def traffic_probe(reps: int):
+    """The roofline kernel's rotation plus a plain copy of known size, for the
+    FETCH_SIZE / WRITE_SIZE counter runs (the copy calibrates the counters)."""
+    import torch
+
+    from dracort_amd.runtime.decode import LlamaShape, synthetic_layer_set
+
+    shape = LlamaShape(n_layers=32)
+    ls = synthetic_layer_set(shape, seed=0, device="cuda")
+    dominant_kernel_roofline(ls, reps)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"traffic probe: {reps} copies of {src.numel()} bytes")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -182,6 +275,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--roofline-reps", type=int, default=20)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--suite", action="store_true", help="measure configurations 1, 2, 4, 5 (one JSON line each)")
+    ap.add_argument("--traffic-probe", action="store_true", help="run only the roofline rotation + a 256 MB copy")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -200,6 +295,13 @@ def main() -> int:
         log("no GPU visible")
         return 1
     torch.cuda.set_device(0)
+    if args.suite:
+        for line in suite(args.roofline_reps):
+            print(json.dumps(line), flush=True)
+        return 0
+    if args.traffic_probe:
+        traffic_probe(args.roofline_reps)
+        return 0
     shape = LlamaShape()
     t0 = time.time()
     ls = synthetic_layer_set(shape, seed=args.seed, device="cuda")

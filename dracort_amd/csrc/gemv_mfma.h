@@ -1,0 +1,347 @@
+// Small-batch decode GEMV (2..16 activation rows) on the matrix cores.
+//
+//   y[m, n] = sum_k x[m, k] * W[n, k],  m < M <= 16
+//
+// With M tokens every decoded weight serves M products, so the products go to
+// v_mfma_f32_16x16x32_bf16: A = the activations (16 token rows x 32 k, rows
+// past M are zero), B = the codes of 16 weight rows (exact in bf16 as
+// 128 + code, one v_perm_b32 per pair), one MFMA per 32-element scale group
+// (a Q4_K sub-block, a Q4_0 block).  Each group's result is scaled on the
+// VALU:  acc += a * (D - (128 + off) S) + b * S,  where w = a (code - off) + b, S =
+// sum_k x (one more MFMA per group against B = all ones, shared by the
+// wave's weight rows).  float32 activations are split into three bf16
+// planes and take three MFMAs per group, against unbiased codes.
+//
+// Grid: a workgroup owns TPW tiles of 16 weight rows; four waves per tile
+// split K (wave ks takes 256-element chunks ks, ks + 4, ...), reading their
+// codes straight into registers (lane l decodes row l % 16, k-slice l / 16 of
+// the MFMA layout) with the next chunk's loads in flight, and their partial
+// 16 x 16 tiles are summed through LDS at the end.  Modes as the other
+// decode GEMVs: kPlain (up to 4 matrices, every row count a multiple of 16),
+// kSwiGLU (gate and up tiles side by side), kResid.
+#pragma once
+
+#include "gemv_stream.h"
+
+namespace draco {
+
+typedef __bf16 mf_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float mf_f32x4 __attribute__((ext_vector_type(4)));
+
+// Codes of one lane for one 256-element chunk: 8 groups x 8 codes (2 dwords
+// of one byte per code), plus what the group coefficients need.
+template <int QT> struct MfChunk;
+template <> struct MfChunk<kQ4_K> { uint4 head; uint32_t qs[4][2]; };    // qs bytes 32p + 8q .. +8, p = 0..3
+template <> struct MfChunk<kQ4_0> { uint32_t d[8]; uint32_t qs[8][2]; };  // per block: f16 d, 8 qs bytes
+
+// Element offset (within the 256-element chunk) of group g's k-slice q.
+template <int QT>
+__device__ __forceinline__ int mf_pos(int g, int q) {
+  if constexpr (QT == kQ4_K) return 64 * (g >> 1) + 32 * (g & 1) + 8 * q;
+  return 32 * g + 8 * q;
+}
+
+// The lane's codes of one chunk; `rowoff` is the byte offset of the lane's
+// weight row within the matrix buffer (a per-lane vector offset).
+template <int QT>
+__device__ __forceinline__ MfChunk<QT> mf_load(__amdgpu_buffer_rsrc_t rsrc, int rowoff, int chunk, int q) {
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  MfChunk<QT> c;
+  if constexpr (QT == kQ4_K) {
+    const int base = rowoff + chunk * 144;
+    const v4i h = __builtin_amdgcn_raw_buffer_load_b128(rsrc, base, 0, 0);
+    c.head = uint4{(uint32_t)h.x, (uint32_t)h.y, (uint32_t)h.z, (uint32_t)h.w};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const v2i t = __builtin_amdgcn_raw_buffer_load_b64(rsrc, base + 16 + 32 * p + 8 * q, 0, 0);
+      c.qs[p][0] = (uint32_t)t.x;
+      c.qs[p][1] = (uint32_t)t.y;
+    }
+  } else {
+    // eight 18-byte blocks; lane slice q reads qs bytes 8 (q & 1) .. + 8 (low
+    // nibbles for q < 2, high nibbles for q >= 2) -- unaligned 8-byte loads
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const int base = rowoff + (chunk * 8 + g) * 18;
+      c.d[g] = (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rsrc, base, 0, 0);
+      const v2i t = __builtin_amdgcn_raw_buffer_load_b64(rsrc, base + 2 + 8 * (q & 1), 0, 0);
+      c.qs[g][0] = (uint32_t)t.x;
+      c.qs[g][1] = (uint32_t)t.y;
+    }
+  }
+  return c;
+}
+
+// B operand of group g: 8 codes as bf16 (128 + code), element order of the k-slice.
+template <int QT>
+__device__ __forceinline__ mf_bf16x8 mf_codes(const MfChunk<QT>& c, int g, int q) {
+  uint32_t w0, w1;
+  if constexpr (QT == kQ4_K) {
+    w0 = (g & 1) ? nib_hi(c.qs[g >> 1][0]) : nib_lo(c.qs[g >> 1][0]);
+    w1 = (g & 1) ? nib_hi(c.qs[g >> 1][1]) : nib_lo(c.qs[g >> 1][1]);
+  } else {
+    const bool hi = q >= 2;
+    w0 = hi ? nib_hi(c.qs[g][0]) : nib_lo(c.qs[g][0]);
+    w1 = hi ? nib_hi(c.qs[g][1]) : nib_lo(c.qs[g][1]);
+  }
+  const uint32_t v[4] = {code_pair_lo(w0), code_pair_hi(w0), code_pair_lo(w1), code_pair_hi(w1)};
+  return __builtin_bit_cast(mf_bf16x8, v);
+}
+
+// B operand without the 128 bias: the codes themselves as bf16 (exact small
+// integers; byte -> float -> upper half of the float bits), used with float32
+// activations, whose three-plane products otherwise lose too many bits in the
+// cancellation of the bias.
+template <int QT>
+__device__ __forceinline__ mf_bf16x8 mf_codes_exact(const MfChunk<QT>& c, int g, int q) {
+  uint32_t w0, w1;
+  if constexpr (QT == kQ4_K) {
+    w0 = (g & 1) ? nib_hi(c.qs[g >> 1][0]) : nib_lo(c.qs[g >> 1][0]);
+    w1 = (g & 1) ? nib_hi(c.qs[g >> 1][1]) : nib_lo(c.qs[g >> 1][1]);
+  } else {
+    const bool hi = q >= 2;
+    w0 = hi ? nib_hi(c.qs[g][0]) : nib_lo(c.qs[g][0]);
+    w1 = hi ? nib_hi(c.qs[g][1]) : nib_lo(c.qs[g][1]);
+  }
+  uint32_t v[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t w = i == 0 ? w0 : w1;
+    v[2 * i] = (__float_as_uint(ubyte_f(w, 0)) >> 16) | (__float_as_uint(ubyte_f(w, 1)) & 0xFFFF0000u);
+    v[2 * i + 1] = (__float_as_uint(ubyte_f(w, 2)) >> 16) | (__float_as_uint(ubyte_f(w, 3)) & 0xFFFF0000u);
+  }
+  return __builtin_bit_cast(mf_bf16x8, v);
+}
+
+// Group coefficients: w = a * (code - off) + b; off folds Q4_0's code offset
+// into the bias subtraction below (one cancellation instead of two).
+template <int QT> struct MfOff { static constexpr float value = QT == kQ4_0 ? 8.f : 0.f; };
+
+template <int QT>
+__device__ __forceinline__ void mf_coeffs(const MfChunk<QT>& c, float (&a)[8], float (&cb)[8]) {
+  if constexpr (QT == kQ4_K) {
+    const float d = f16_bits_to_f32(c.head.x), dmin = f16_bits_to_f32(c.head.x >> 16);
+    const uint32_t s0 = c.head.y, s1 = c.head.z, s2 = c.head.w;
+    const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, m_lo = s1 & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const float sc = ubyte_f(g < 4 ? sc_lo : sc_hi, g & 3);
+      const float mn = ubyte_f(g < 4 ? m_lo : m_hi, g & 3);
+      a[g] = d * sc;
+      cb[g] = -(dmin * mn);
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      a[g] = f16_bits_to_f32(c.d[g]);
+      cb[g] = 0.f;
+    }
+  }
+}
+
+// A operand: 8 activations of token row m at element p of the chunk (zero
+// past M).  float32 activations are split exactly enough into three bf16
+// planes x = hi + mid + lo (each the round-to-nearest bf16 of what the
+// previous ones leave; |x - hi - mid - lo| <= 2^-27 |x|): a two-plane split
+// (2^-18) is not enough for the 1e-3 elementwise bound on outputs near zero.
+template <bool XBF16>
+__device__ __forceinline__ void mf_load_x(const void* __restrict__ x, int k, int m, int M, int p,
+                                          mf_bf16x8 (&pl)[XBF16 ? 1 : 3]) {
+  if constexpr (XBF16) {
+    uint4 v = {0u, 0u, 0u, 0u};
+    if (m < M) v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + (size_t)m * k + p);
+    pl[0] = __builtin_bit_cast(mf_bf16x8, v);
+  } else {
+    float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (m < M) {
+      const float4* s = reinterpret_cast<const float4*>(static_cast<const float*>(x) + (size_t)m * k + p);
+      const float4 u = s[0], w = s[1];
+      f[0] = u.x; f[1] = u.y; f[2] = u.z; f[3] = u.w; f[4] = w.x; f[5] = w.y; f[6] = w.z; f[7] = w.w;
+    }
+    uint32_t b[3][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t part[3][2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        float rem = f[2 * i + e];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          part[j][e] = f32_to_bf16_rne(rem);
+          rem -= __uint_as_float(part[j][e] << 16);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 3; ++j) b[j][i] = part[j][0] | (part[j][1] << 16);
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) pl[j] = __builtin_bit_cast(mf_bf16x8, b[j]);
+  }
+}
+
+template <int QT, bool XBF16, int MODE, int TPW>
+__global__ __launch_bounds__(TPW * 256) void gemv_mfma_kernel(StreamJob job) {
+  constexpr int NR = MODE == kSwiGLU ? 2 : 1;
+  __shared__ mf_f32x4 part[TPW][4][NR][64];
+  const int lane = threadIdx.x & 63;
+  // wave-uniform indices in scalar registers (the buffer resources built from
+  // them must be uniform, or every load becomes a waterfall loop)
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = wid >> 2, ks = wid & 3;
+  const int row0 = (blockIdx.x * TPW + t) * 16;
+  const int q = lane >> 4, nl = lane & 15;
+  const int k = job.k, M = job.m;
+  const int chunks = k >> 8;
+
+  // the tile's matrix (a tile never straddles two: every row count is a
+  // multiple of 16) and the lane's row in it (clamped; rows past the end are
+  // computed, not stored)
+  const int trow = min(row0, job.rows - 1);
+  int mat = 0, lrow0 = trow;
+  if constexpr (MODE == kPlain) row_of(job, trow, mat, lrow0);
+  __amdgpu_buffer_rsrc_t rs[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int mm = NR == 2 ? r : mat;
+    rs[r] = make_rsrc(job.w[mm], (uint32_t)((int64_t)job.n[mm] * job.row_bytes));
+  }
+  const int rowoff = (int)((int64_t)min(lrow0 + nl, job.n[NR == 2 ? 0 : mat] - 1) * job.row_bytes);
+
+  mf_f32x4 acc[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) acc[r] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t ones[4] = {kOnePair, kOnePair, kOnePair, kOnePair};
+  const mf_bf16x8 bones = __builtin_bit_cast(mf_bf16x8, ones);
+  // software pipeline: the activations and codes of chunk c + 4 are loaded
+  // while chunk c is multiplied
+  constexpr int NP = XBF16 ? 1 : 3;
+  MfChunk<QT> cur[NR], nxt[NR];
+  mf_bf16x8 xc[8][NP], xn[8][NP];
+  int c = ks;
+  if (c < chunks) {
+#pragma unroll
+    for (int g = 0; g < 8; ++g) mf_load_x<XBF16>(job.x, k, nl, M, c * 256 + mf_pos<QT>(g, q), xc[g]);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) cur[r] = mf_load<QT>(rs[r], rowoff, c, q);
+  }
+  for (; c < chunks; c += 4) {
+    if (c + 4 < chunks) {
+#pragma unroll
+      for (int g = 0; g < 8; ++g) mf_load_x<XBF16>(job.x, k, nl, M, (c + 4) * 256 + mf_pos<QT>(g, q), xn[g]);
+#pragma unroll
+      for (int r = 0; r < NR; ++r) nxt[r] = mf_load<QT>(rs[r], rowoff, c + 4, q);
+    }
+    float a[NR][8], cb[NR][8];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) mf_coeffs<QT>(cur[r], a[r], cb[r]);
+    const mf_f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    mf_f32x4 sg[8], dg[NR][8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      sg[g] = z;
+#pragma unroll
+      for (int j = NP - 1; j >= 0; --j) sg[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[g][j], bones, sg[g], 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const mf_bf16x8 bc = XBF16 ? mf_codes<QT>(cur[r], g, q) : mf_codes_exact<QT>(cur[r], g, q);
+        dg[r][g] = z;
+#pragma unroll
+        for (int j = NP - 1; j >= 0; --j)
+          dg[r][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[g][j], bc, dg[r][g], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          // sum x * code = D - 128 S, formed with one rounding before it is
+          // scaled (the 128 bias must cancel here, not in the running sum)
+          const float bias = (XBF16 ? kCodeBias : 0.f) + MfOff<QT>::value;
+          const float xcode = fmaf(-bias, sg[g][v], dg[r][g][v]);
+          if constexpr (QT == kQ4_K) acc[r][v] = fmaf(cb[r][g], sg[g][v], acc[r][v]);
+          acc[r][v] = fmaf(a[r][g], xcode, acc[r][v]);
+        }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) cur[r] = nxt[r];
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+#pragma unroll
+      for (int j = 0; j < NP; ++j) xc[g][j] = xn[g][j];
+  }
+
+  // sum the four K-split partial tiles
+#pragma unroll
+  for (int r = 0; r < NR; ++r) part[t][ks][r][lane] = acc[r];
+  __syncthreads();
+  if (ks != 0) return;
+  mf_f32x4 tot[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    tot[r] = part[t][0][r][lane];
+#pragma unroll
+    for (int j = 1; j < 4; ++j) {
+      const mf_f32x4 p = part[t][j][r][lane];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) tot[r][v] += p[v];
+    }
+  }
+  const int orow = row0 + nl;
+  if (orow >= job.rows) return;
+  int omat = 0, olrow = orow;
+  if constexpr (MODE == kPlain) row_of(job, orow, omat, olrow);
+  const int n = job.n[omat];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int m = 4 * q + v;  // D layout: lane l holds rows 4 (l / 16) + v, column l % 16
+    if (m >= M) continue;
+    const size_t o = (size_t)m * n + olrow;
+    if constexpr (MODE == kResid) {
+      const float out = job.resid[o] + tot[0][v];
+      job.resid[o] = out;
+      if (job.resid_bf16) job.resid_bf16[o] = f32_to_bf16_rne(out);
+    } else {
+      float out = tot[0][v];
+      if constexpr (MODE == kSwiGLU) out = silu(tot[0][v]) * tot[1][v];
+      if (MODE == kPlain && job.bias) out += job.bias[olrow];
+      if (job.y[omat]) job.y[omat][o] = out;
+      if (job.yb[omat]) job.yb[omat][o] = f32_to_bf16_rne(out);
+    }
+  }
+}
+
+// Whether the matrix-core GEMV takes this launch: K-quant Q4_K or Q4_0,
+// 2..16 activation rows, K a multiple of 256, every matrix a whole number of
+// 16-row tiles, 32-bit buffer offsets.
+inline bool mfma_gemv_ok(int qtype, const StreamJob& job) {
+  if (!(qtype == kQ4_K || qtype == kQ4_0) || job.m < 2 || job.m > 16 || job.k % 256 != 0) return false;
+  for (int i = 0; i < job.n_mats; ++i) {
+    if (job.n[i] % 16 != 0) return false;
+    if ((int64_t)job.n[i] * job.row_bytes >= ((int64_t)1 << 31)) return false;
+  }
+  return true;
+}
+
+template <int QT, bool XBF16, int MODE>
+static int launch_gemv_mfma(const StreamJob& job, hipStream_t s) {
+  const int tiles = (job.rows + 15) / 16;
+  if (tiles >= 2048) {
+    hipLaunchKernelGGL((gemv_mfma_kernel<QT, XBF16, MODE, 2>), dim3((tiles + 1) / 2), dim3(512), 0, s, job);
+  } else {
+    hipLaunchKernelGGL((gemv_mfma_kernel<QT, XBF16, MODE, 1>), dim3(tiles), dim3(256), 0, s, job);
+  }
+  return check_launch("gemv_mfma");
+}
+
+template <int MODE>
+static int gemv_mfma_dispatch(int qtype, const StreamJob& job, bool xbf16, hipStream_t s) {
+  if (qtype == kQ4_K)
+    return xbf16 ? launch_gemv_mfma<kQ4_K, true, MODE>(job, s) : launch_gemv_mfma<kQ4_K, false, MODE>(job, s);
+  return xbf16 ? launch_gemv_mfma<kQ4_0, true, MODE>(job, s) : launch_gemv_mfma<kQ4_0, false, MODE>(job, s);
+}
+
+}  // namespace draco

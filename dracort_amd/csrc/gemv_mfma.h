@@ -142,22 +142,21 @@ __device__ __forceinline__ void mf_coeffs(const MfChunk<QT>& c, float (&a)[8], f
   }
 }
 
-// A operand: 8 activations of token row m at element p of the chunk (zero
-// past M).  float32 activations are split exactly enough into three bf16
+// A operand: 8 activations of token row m at element p of the chunk.  Rows
+// past M read row M - 1 instead of zeros: row m of the product depends only
+// on row m of A, and rows >= M are never stored.  float32 activations are split exactly enough into three bf16
 // planes x = hi + mid + lo (each the round-to-nearest bf16 of what the
 // previous ones leave; |x - hi - mid - lo| <= 2^-27 |x|): a two-plane split
 // (2^-18) is not enough for the 1e-3 elementwise bound on outputs near zero.
 template <bool XBF16>
-__device__ __forceinline__ void mf_load_x(const void* __restrict__ x, int k, int m, int M, int p,
-                                          mf_bf16x8 (&pl)[XBF16 ? 1 : 3]) {
+__device__ __forceinline__ void mf_load_x(const void* __restrict__ xrow, int p, mf_bf16x8 (&pl)[XBF16 ? 1 : 3]) {
   if constexpr (XBF16) {
-    uint4 v = {0u, 0u, 0u, 0u};
-    if (m < M) v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + (size_t)m * k + p);
+    const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xrow) + p);
     pl[0] = __builtin_bit_cast(mf_bf16x8, v);
   } else {
-    float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (m < M) {
-      const float4* s = reinterpret_cast<const float4*>(static_cast<const float*>(x) + (size_t)m * k + p);
+    float f[8];
+    {
+      const float4* s = reinterpret_cast<const float4*>(static_cast<const float*>(xrow) + p);
       const float4 u = s[0], w = s[1];
       f[0] = u.x; f[1] = u.y; f[2] = u.z; f[3] = u.w; f[4] = w.x; f[5] = w.y; f[6] = w.z; f[7] = w.w;
     }
@@ -180,6 +179,73 @@ __device__ __forceinline__ void mf_load_x(const void* __restrict__ x, int k, int
 #pragma unroll
     for (int j = 0; j < 3; ++j) pl[j] = __builtin_bit_cast(mf_bf16x8, b[j]);
   }
+}
+
+// acc (the lane's 4 values of the 16 x 16 tile) += the products over the
+// 256-element chunks ks, ks + 4, ... < chunks of NR weight rows (buffer
+// resources rs, the lane's row at byte offset rowoff) with the lane's
+// activation row xrow.  Software pipeline: the activations and codes of chunk
+// c + 4 are loaded while chunk c is multiplied.
+template <int QT, bool XBF16, int NR>
+__device__ __forceinline__ void mf_accumulate(const __amdgpu_buffer_rsrc_t (&rs)[NR], int rowoff,
+                                              const void* __restrict__ xrow, int q, int ks, int chunks,
+                                              mf_f32x4 (&acc)[NR]) {
+  const uint32_t ones[4] = {kOnePair, kOnePair, kOnePair, kOnePair};
+  const mf_bf16x8 bones = __builtin_bit_cast(mf_bf16x8, ones);
+  // two buffer sets used alternately (no copies)
+  constexpr int NP = XBF16 ? 1 : 3;
+  MfChunk<QT> wb[2][NR];
+  mf_bf16x8 xb[2][8][NP];
+  auto load_chunk = [&](int slot, int cc) {
+#pragma unroll
+    for (int g = 0; g < 8; ++g) mf_load_x<XBF16>(xrow, cc * 256 + mf_pos<QT>(g, q), xb[slot][g]);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) wb[slot][r] = mf_load<QT>(rs[r], rowoff, cc, q);
+  };
+  auto compute_chunk = [&](int slot) {
+    float a[NR][8], cb[NR][8];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) mf_coeffs<QT>(wb[slot][r], a[r], cb[r]);
+    const mf_f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    mf_f32x4 sg[8], dg[NR][8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      sg[g] = z;
+#pragma unroll
+      for (int j = NP - 1; j >= 0; --j)
+        sg[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[slot][g][j], bones, sg[g], 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const mf_bf16x8 bc = XBF16 ? mf_codes<QT>(wb[slot][r], g, q) : mf_codes_exact<QT>(wb[slot][r], g, q);
+        dg[r][g] = z;
+#pragma unroll
+        for (int j = NP - 1; j >= 0; --j)
+          dg[r][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[slot][g][j], bc, dg[r][g], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          // sum x * (code - off) = D - (bias + off) S, formed with one rounding
+          // before it is scaled (the bias must cancel here, not in the running sum)
+          const float bias = (XBF16 ? kCodeBias : 0.f) + MfOff<QT>::value;
+          const float xcode = fmaf(-bias, sg[g][v], dg[r][g][v]);
+          if constexpr (QT == kQ4_K) acc[r][v] = fmaf(cb[r][g], sg[g][v], acc[r][v]);
+          acc[r][v] = fmaf(a[r][g], xcode, acc[r][v]);
+        }
+  };
+  if (ks < chunks) load_chunk(0, ks);
+  for (int c = ks; c < chunks; c += 8) {
+    if (c + 4 < chunks) load_chunk(1, c + 4);
+    compute_chunk(0);
+    if (c + 4 >= chunks) break;
+    if (c + 8 < chunks) load_chunk(0, c + 8);
+    compute_chunk(1);
+  }
+
 }
 
 template <int QT, bool XBF16, int MODE, int TPW>
@@ -213,66 +279,8 @@ __global__ __launch_bounds__(TPW * 256) void gemv_mfma_kernel(StreamJob job) {
   mf_f32x4 acc[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) acc[r] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
-  const uint32_t ones[4] = {kOnePair, kOnePair, kOnePair, kOnePair};
-  const mf_bf16x8 bones = __builtin_bit_cast(mf_bf16x8, ones);
-  // software pipeline: the activations and codes of chunk c + 4 are loaded
-  // while chunk c is multiplied
-  constexpr int NP = XBF16 ? 1 : 3;
-  MfChunk<QT> cur[NR], nxt[NR];
-  mf_bf16x8 xc[8][NP], xn[8][NP];
-  int c = ks;
-  if (c < chunks) {
-#pragma unroll
-    for (int g = 0; g < 8; ++g) mf_load_x<XBF16>(job.x, k, nl, M, c * 256 + mf_pos<QT>(g, q), xc[g]);
-#pragma unroll
-    for (int r = 0; r < NR; ++r) cur[r] = mf_load<QT>(rs[r], rowoff, c, q);
-  }
-  for (; c < chunks; c += 4) {
-    if (c + 4 < chunks) {
-#pragma unroll
-      for (int g = 0; g < 8; ++g) mf_load_x<XBF16>(job.x, k, nl, M, (c + 4) * 256 + mf_pos<QT>(g, q), xn[g]);
-#pragma unroll
-      for (int r = 0; r < NR; ++r) nxt[r] = mf_load<QT>(rs[r], rowoff, c + 4, q);
-    }
-    float a[NR][8], cb[NR][8];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) mf_coeffs<QT>(cur[r], a[r], cb[r]);
-    const mf_f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    mf_f32x4 sg[8], dg[NR][8];
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-      sg[g] = z;
-#pragma unroll
-      for (int j = NP - 1; j >= 0; --j) sg[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[g][j], bones, sg[g], 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const mf_bf16x8 bc = XBF16 ? mf_codes<QT>(cur[r], g, q) : mf_codes_exact<QT>(cur[r], g, q);
-        dg[r][g] = z;
-#pragma unroll
-        for (int j = NP - 1; j >= 0; --j)
-          dg[r][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xc[g][j], bc, dg[r][g], 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < 8; ++g)
-#pragma unroll
-      for (int r = 0; r < NR; ++r)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          // sum x * code = D - 128 S, formed with one rounding before it is
-          // scaled (the 128 bias must cancel here, not in the running sum)
-          const float bias = (XBF16 ? kCodeBias : 0.f) + MfOff<QT>::value;
-          const float xcode = fmaf(-bias, sg[g][v], dg[r][g][v]);
-          if constexpr (QT == kQ4_K) acc[r][v] = fmaf(cb[r][g], sg[g][v], acc[r][v]);
-          acc[r][v] = fmaf(a[r][g], xcode, acc[r][v]);
-        }
-#pragma unroll
-    for (int r = 0; r < NR; ++r) cur[r] = nxt[r];
-#pragma unroll
-    for (int g = 0; g < 8; ++g)
-#pragma unroll
-      for (int j = 0; j < NP; ++j) xc[g][j] = xn[g][j];
-  }
+  const void* xrow = static_cast<const uint8_t*>(job.x) + (size_t)min(nl, M - 1) * k * (XBF16 ? 2 : 4);
+  mf_accumulate<QT, XBF16, NR>(rs, rowoff, xrow, q, ks, chunks, acc);
 
   // sum the four K-split partial tiles
 #pragma unroll

@@ -18,8 +18,16 @@
 //     (expert, token) assignment.
 //  4. moe_combine_kernel: y[t] = sum over the token's slots in ascending
 //     expert order of weight * down_out, the reference's index_add_ order.
+//
+// Q4_K and Q4_0 experts with 256-divisible dims take the matrix-core forms of
+// steps 2 and 3 (moe_up_mfma_kernel, moe_down_mfma_kernel): a workgroup owns
+// one 16-row weight tile of one expert, four waves split K, and each gathered
+// tile of 16 tokens is one 16 x 16 MFMA output tile (the decode GEMV's
+// mf_accumulate), so an expert's weights are read once per 16 tokens instead
+// of once per token row of the register core.
 #include "draco_internal.h"
 #include "gemv_core.h"
+#include "gemv_mfma.h"
 
 namespace draco {
 
@@ -213,6 +221,94 @@ __global__ __launch_bounds__(256) void moe_down_kernel(ExpertPtrs wd, int H, int
   }
 }
 
+// h[off + t0 + m, :] = silu(x_t W_gate[e]^T) * (x_t W_up[e]^T) for the
+// expert's tokens t = assign_tok[off + t0 + m], 16 tokens per pass.
+template <int QT, bool XBF16>
+__global__ __launch_bounds__(256) void moe_up_mfma_kernel(ExpertPtrs wg, ExpertPtrs wu, const void* __restrict__ x,
+                                                          int H, int I, MoeWs ws) {
+  __shared__ mf_f32x4 part[4][2][64];
+  const int e = blockIdx.y;
+  const int cnt = ws.counts[e];
+  if (cnt == 0) return;
+  const int off = ws.offsets[e];
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, nl = lane & 15;
+  const int row0 = blockIdx.x * 16;  // I is a multiple of 16 and the grid covers it exactly
+  const uint32_t row_bytes = (uint32_t)(H / Fmt<QT>::QK) * Fmt<QT>::BYTES;
+  const __amdgpu_buffer_rsrc_t rs[2] = {make_rsrc(wg.p[e], (uint32_t)I * row_bytes),
+                                        make_rsrc(wu.p[e], (uint32_t)I * row_bytes)};
+  const int rowoff = (int)((uint32_t)(row0 + nl) * row_bytes);
+  const size_t xstride = (size_t)H * (XBF16 ? 2 : 4);
+  for (int t0 = 0; t0 < cnt; t0 += 16) {
+    const int mt = min(16, cnt - t0);
+    // lanes of token rows past the expert's count repeat its last token
+    const int tok = ws.assign_tok[off + t0 + min(nl, mt - 1)];
+    const void* xrow = static_cast<const uint8_t*>(x) + (size_t)tok * xstride;
+    mf_f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    mf_accumulate<QT, XBF16, 2>(rs, rowoff, xrow, q, ks, H >> 8, acc);
+    part[ks][0][lane] = acc[0];
+    part[ks][1][lane] = acc[1];
+    __syncthreads();
+    if (ks == 0) {
+      mf_f32x4 g = part[0][0][lane], u = part[0][1][lane];
+#pragma unroll
+      for (int j = 1; j < 4; ++j) {
+        const mf_f32x4 pg = part[j][0][lane], pu = part[j][1][lane];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) { g[v] += pg[v]; u[v] += pu[v]; }
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = 4 * q + v;  // D layout: lane l holds token rows 4 (l / 16) + v, weight row l % 16
+        if (m < mt) ws.h[(size_t)(off + t0 + m) * I + row0 + nl] = silu_f(g[v]) * u[v];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// yk[off + t0 + m, :] = h[off + t0 + m, :] W_down[e]^T, 16 assignment rows per
+// pass (float32 h: three bf16 planes per MFMA group).
+template <int QT>
+__global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertPtrs wd, int H, int I, MoeWs ws) {
+  __shared__ mf_f32x4 part[4][64];
+  const int e = blockIdx.y;
+  const int cnt = ws.counts[e];
+  if (cnt == 0) return;
+  const int off = ws.offsets[e];
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, nl = lane & 15;
+  const int row0 = blockIdx.x * 16;  // H is a multiple of 16 and the grid covers it exactly
+  const uint32_t row_bytes = (uint32_t)(I / Fmt<QT>::QK) * Fmt<QT>::BYTES;
+  const __amdgpu_buffer_rsrc_t rs[1] = {make_rsrc(wd.p[e], (uint32_t)H * row_bytes)};
+  const int rowoff = (int)((uint32_t)(row0 + nl) * row_bytes);
+  for (int t0 = 0; t0 < cnt; t0 += 16) {
+    const int mt = min(16, cnt - t0);
+    const float* xrow = ws.h + (size_t)(off + t0 + min(nl, mt - 1)) * I;
+    mf_f32x4 acc[1] = {{0.f, 0.f, 0.f, 0.f}};
+    mf_accumulate<QT, false, 1>(rs, rowoff, xrow, q, ks, I >> 8, acc);
+    part[ks][lane] = acc[0];
+    __syncthreads();
+    if (ks == 0) {
+      mf_f32x4 tot = part[0][lane];
+#pragma unroll
+      for (int j = 1; j < 4; ++j) {
+        const mf_f32x4 p = part[j][lane];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tot[v] += p[v];
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = 4 * q + v;
+        if (m < mt) ws.yk[(size_t)(off + t0 + m) * H + row0 + nl] = tot[v];
+      }
+    }
+    __syncthreads();
+  }
+}
+
 __global__ __launch_bounds__(256) void moe_combine_kernel(float* __restrict__ y, int H, int k, MoeWs ws) {
   const int t = blockIdx.y;
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
@@ -233,6 +329,27 @@ static int launch_moe(const ExpertPtrs& wg, const ExpertPtrs& wu, const ExpertPt
   constexpr int R = 1;
   hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), 0, s, logits, T, E, k, ws);
   if (int rc = check_launch("moe_route")) return rc;
+  if constexpr (QT == kQ4_K || QT == kQ4_0) {
+    // matrix-core experts: K a whole number of 256-element chunks, whole
+    // 16-row tiles, 32-bit buffer offsets within one expert matrix
+    const int64_t up_bytes = (int64_t)I * (H / Fmt<QT>::QK) * Fmt<QT>::BYTES;
+    const int64_t down_bytes = (int64_t)H * (I / Fmt<QT>::QK) * Fmt<QT>::BYTES;
+    if (H % 256 == 0 && I % 256 == 0 && up_bytes < ((int64_t)1 << 31) && down_bytes < ((int64_t)1 << 31)) {
+      if (xbf16)
+        hipLaunchKernelGGL((moe_up_mfma_kernel<QT, true>), dim3((unsigned)(I / 16), (unsigned)E), dim3(256), 0, s,
+                           wg, wu, x, H, I, ws);
+      else
+        hipLaunchKernelGGL((moe_up_mfma_kernel<QT, false>), dim3((unsigned)(I / 16), (unsigned)E), dim3(256), 0, s,
+                           wg, wu, x, H, I, ws);
+      if (int rc = check_launch("moe_up_mfma")) return rc;
+      hipLaunchKernelGGL((moe_down_mfma_kernel<QT>), dim3((unsigned)(H / 16), (unsigned)E), dim3(256), 0, s, wd, H,
+                         I, ws);
+      if (int rc = check_launch("moe_down_mfma")) return rc;
+      hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, s, y,
+                         H, k, ws);
+      return check_launch("moe_combine");
+    }
+  }
   const dim3 gup((unsigned)((I + 4 * R - 1) / (4 * R)), (unsigned)E);
   if (xbf16)
     hipLaunchKernelGGL((moe_up_kernel<QT, true, R>), gup, dim3(256), 0, s, wg, wu, x, H, I, ws);

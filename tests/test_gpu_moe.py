@@ -60,6 +60,15 @@ def test_moe_edge_routing():
     check_close(y, ref, "moe top1 f32")
 
 
+@pytest.mark.parametrize("qtype", [Q4_K, Q4_0])
+def test_moe_matrix_core_f32(qtype):
+    """float32 hidden states on the matrix-core experts (three bf16 planes),
+    ragged per-expert counts (33 tokens, top-2 over 5 experts)."""
+    print(f"moe {NAMES[qtype]} f32 T=33 E=5", flush=True)
+    y, ref = _run(qtype, 33, 512, 768, 5, 2, seed=24 + qtype, xdtype=torch.float32)
+    check_close(y, ref, f"moe {NAMES[qtype]} f32")
+
+
 def test_moe_mixtral_shape_subset():
     """Mixtral-8x7B expert shapes (H=4096, I=14336), Q4_K, 64 tokens, top-2;
     two experts so the fp64 oracle stays small."""

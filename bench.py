@@ -92,7 +92,7 @@ def dominant_kernel_roofline(ls, reps):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
     return {
-        "kernel": "gemv_x1_kernel<Q4_K> (decode GEMV, M = 1, bf16 x) on a 14336 x 4096 Q4_K weight",
+        "kernel": "gemv_x1p_kernel<Q4_K> (persistent decode GEMV, M = 1, bf16 x) on a 14336 x 4096 Q4_K weight",
         "bound": "hbm",
         "achieved": round(achieved, 1),
         "peak": PEAK_HBM_GBS,

@@ -28,6 +28,8 @@
 // matrices sharing x, kSwiGLU, kResid).
 #pragma once
 
+#include <climits>
+
 #include "gemv_mfma.h"
 #include "gemv_stream.h"
 
@@ -145,22 +147,21 @@ __device__ __forceinline__ int x1_slot_of_chunk(int c) {  // natural chunk (8 bf
 
 inline size_t tile_x_lds_bytes_q4k(int k) { return (size_t)k * 2 + (size_t)(k / 32) * 2 * sizeof(float); }
 
-inline size_t x1_lds_bytes(int qtype, int k) {
+__host__ __device__ inline size_t x1_lds_bytes(int qtype, int k) {
   const int steps = ((k >> 6) + 63) >> 6;
   const int g = qtype == kQ4_K ? 2 : 4;
   return (size_t)steps * 512 * 16 + (size_t)steps * g * 64 * 4;
 }
 
-// Every thread of the workgroup calls this; it ends in a barrier.
+// the persistent kernel's LDS: the image, its sums and a 4 KB pad
+inline size_t x1p_lds_bytes(int qtype, int k) { return x1_lds_bytes(qtype, k) + 256 * 16; }
+
+// Group sums of the staged image (after the barrier that ends the stores);
+// ends in a barrier.
 template <int QT>
-__device__ __forceinline__ void x1_stage(uint4* lds, const uint16_t* __restrict__ x, int k) {
+__device__ __forceinline__ void x1_stage_sums(uint4* lds, int k) {
   constexpr int G = X1Fmt<QT>::G, CPG = X1Fmt<QT>::GL / 8;
   const int units = k >> 6, steps = (units + 63) >> 6;
-  const int chunks = k >> 3;
-  const uint4* xs = reinterpret_cast<const uint4*>(x);
-  for (int c = threadIdx.x; c < chunks; c += blockDim.x)
-    lds[(c >> 9) * 512 + x1_slot_of_chunk<QT>(c & 511)] = xs[c];
-  __syncthreads();
   float* sums = reinterpret_cast<float*>(lds + steps * 512);
   for (int i = threadIdx.x; i < units * G; i += blockDim.x) {
     const int u = i / G, g = i - u * G;
@@ -177,6 +178,35 @@ __device__ __forceinline__ void x1_stage(uint4* lds, const uint16_t* __restrict_
     sums[(st * G + g) * 64 + l] = t;
   }
   __syncthreads();
+}
+
+// Every thread of the workgroup calls this; it ends in a barrier.
+template <int QT>
+__device__ __forceinline__ void x1_stage(uint4* lds, const uint16_t* __restrict__ x, int k) {
+  const int chunks = k >> 3;
+  const uint4* xs = reinterpret_cast<const uint4*>(x);
+  for (int c = threadIdx.x; c < chunks; c += blockDim.x)
+    lds[(c >> 9) * 512 + x1_slot_of_chunk<QT>(c & 511)] = xs[c];
+  __syncthreads();
+  x1_stage_sums<QT>(lds, k);
+}
+
+// The same from chunks threadIdx.x and threadIdx.x + 256 already in
+// registers (workgroups of 256 threads, K <= 4096).  Chunks past K go to a
+// 4 KB pad after the image (x1p_lds_bytes) instead of being skipped: with an
+// unconditional store the loads stay where they were issued instead of being
+// sunk into a branch behind the weight loads.
+template <int QT>
+__device__ __forceinline__ void x1_stage_regs(uint4* lds, const uint4 (&xr)[2], int k) {
+  const int chunks = k >> 3;
+  const int pad = (int)(x1_lds_bytes(QT, k) / 16);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = (int)threadIdx.x + 256 * j;
+    lds[c < chunks ? (c >> 9) * 512 + x1_slot_of_chunk<QT>(c & 511) : pad + (int)threadIdx.x] = xr[j];
+  }
+  __syncthreads();
+  x1_stage_sums<QT>(lds, k);
 }
 
 // The lane's activations of step s from the LDS image (zero when !live).
@@ -349,79 +379,136 @@ __global__ __launch_bounds__(256, OCC) void gemv_x1_kernel(StreamJob job) {
 
 // Persistent form for rows of one step (K <= 4096): a fixed grid of waves,
 // wave w computes rows w, w + W, w + 2W, ... (W = all waves) with the packed
-// bytes of the next PF rows in flight while it multiplies the current one, so
-// the loads are issued at the pace the math consumes them (instead of every
-// wave requesting its rows at once and all of them finishing together).  The
-// activations (the bf16 LDS image) are read into registers once.
+// bytes of the next PF rows in flight while it multiplies the current one.
+// Issue order keeps every vector-memory wait exact: the activations are
+// requested first, then the first PF rows; each iteration requests row i + PF
+// (through an empty buffer resource once past the wave's last row, so the
+// load instruction is always issued and returns zeros without touching
+// memory) before it multiplies row i; results are kept in lane i % 64 of one
+// register and stored after the loop, so no store sits between the loads.
 template <int QT, bool DL, int MODE, int PF>
 __global__ __launch_bounds__(256) void gemv_x1p_kernel(StreamJob job) {
   constexpr int NR = MODE == kSwiGLU ? 2 : 1;
+  constexpr int NB = PF + 1;
   extern __shared__ uint4 x1_smem[];
   const int lane = threadIdx.x & 63;
   const int W = gridDim.x * 4;
   const int w = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  x1_stage<QT>(x1_smem, static_cast<const uint16_t*>(job.x), job.k);
   const int nrow = job.rows > w ? (job.rows - w + W - 1) / W : 0;
-  if (nrow == 0) return;
-  const int units = job.k >> 6;
+  const int k = job.k;
+  const int units = k >> 6;
   const bool live = lane < units;
   const int ul = live ? lane : units - 1;
-  const X1Lane lc = x1_lane<QT>(lane);
-  X1Act xa;
-  x1_read_lds<QT>(x1_smem, job.k, 0, lane, live, xa);
+
+  // kPlain: up to four matrices with their rows concatenated; row r belongs
+  // to matrix (r >= c1) + (r >= c2) + (r >= c3)
+  int c1 = INT_MAX, c2 = INT_MAX, c3 = INT_MAX;
+  if constexpr (MODE == kPlain) {
+    if (job.n_mats > 1) c1 = job.n[0];
+    if (job.n_mats > 2) c2 = c1 + job.n[1];
+    if (job.n_mats > 3) c3 = c2 + job.n[2];
+  }
+  constexpr int NM = MODE == kPlain ? kMaxMats : NR;
+  __amdgpu_buffer_rsrc_t rs[NM];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+    rs[m] = make_rsrc(job.w[m], m < job.n_mats || NR == 2 ? (uint32_t)((int64_t)job.n[m] * job.row_bytes) : 0u);
+  const __amdgpu_buffer_rsrc_t empty = make_rsrc(job.w[0], 0u);
 
   auto rowbuf = [&](int i, int q) {
-    int mat = 0, lrow = w + i * W;
-    if constexpr (MODE == kPlain) row_of(job, lrow, mat, lrow);
-    const int m = NR == 2 ? q : mat;
     X1Buf b;
-    b.rsrc = make_rsrc(job.w[m], (uint32_t)((int64_t)job.n[m] * job.row_bytes));
-    b.soff = (int)((int64_t)lrow * job.row_bytes);
+    if (i >= nrow) {
+      b.rsrc = empty;
+      b.soff = 0;
+      return b;
+    }
+    const int r = w + i * W;
+    if constexpr (MODE == kPlain) {
+      const int mat = (r >= c1) + (r >= c2) + (r >= c3);
+      const int base = mat == 0 ? 0 : mat == 1 ? c1 : mat == 2 ? c2 : c3;
+      b.rsrc = mat == 0 ? rs[0] : mat == 1 ? rs[1] : mat == 2 ? rs[2] : rs[3];
+      b.soff = (r - base) * job.row_bytes;
+    } else {
+      b.rsrc = rs[q];
+      b.soff = r * job.row_bytes;
+    }
     return b;
   };
-  X1Raw<QT> buf[PF][NR];
+
+  // 1. activations (at most two 16-byte chunks per thread), then the first rows
+  uint4 xr[2];
+  {
+    const uint4* xs = static_cast<const uint4*>(job.x);
+    const int chunks = k >> 3;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) xr[j] = xs[min((int)threadIdx.x + 256 * j, chunks - 1)];
+  }
+  X1Raw<QT> buf[NB][NR];
 #pragma unroll
   for (int p = 0; p < PF; ++p)
 #pragma unroll
-    for (int q = 0; q < NR; ++q) buf[p][q] = x1_load<QT, DL>(rowbuf(min(p, nrow - 1), q), ul);
+    for (int q = 0; q < NR; ++q) buf[p][q] = x1_load<QT, DL>(rowbuf(p, q), ul);
 
-  for (int i0 = 0; i0 < nrow; i0 += PF) {
+  // 2. the LDS image and group sums; the lane's activations into registers
+  x1_stage_regs<QT>(x1_smem, xr, k);
+  if (nrow == 0) return;
+  const X1Lane lc = x1_lane<QT>(lane);
+  X1Act xa;
+  x1_read_lds<QT>(x1_smem, k, 0, lane, live, xa);
+
+  // 3. rows
+  float res = 0.f;
+  auto flush = [&](int i0, int cnt) {
+    const int i = i0 + lane;
+    if (lane >= cnt) return;
+    const int r = w + i * W;
+    int mat = 0, lrow = r;
+    if constexpr (MODE == kPlain) {
+      mat = (r >= c1) + (r >= c2) + (r >= c3);
+      lrow = r - (mat == 0 ? 0 : mat == 1 ? c1 : mat == 2 ? c2 : c3);
+    }
+    if constexpr (MODE == kResid) {
+      const float out = job.resid[lrow] + res;
+      job.resid[lrow] = out;
+      if (job.resid_bf16) job.resid_bf16[lrow] = f32_to_bf16_rne(out);
+    } else {
+      float out = res;
+      if (MODE == kPlain && job.bias) out += job.bias[lrow];
+      float* y = job.y[0];
+      uint16_t* yb = job.yb[0];
+      if constexpr (MODE == kPlain) {
+        y = mat == 0 ? job.y[0] : mat == 1 ? job.y[1] : mat == 2 ? job.y[2] : job.y[3];
+        yb = mat == 0 ? job.yb[0] : mat == 1 ? job.yb[1] : mat == 2 ? job.yb[2] : job.yb[3];
+      }
+      if (y) y[lrow] = out;
+      if (yb) yb[lrow] = f32_to_bf16_rne(out);
+    }
+  };
+  for (int i0 = 0; i0 < nrow; i0 += NB) {
 #pragma unroll
-    for (int p = 0; p < PF; ++p) {
+    for (int p = 0; p < NB; ++p) {
       const int i = i0 + p;
+#pragma unroll
+      for (int q = 0; q < NR; ++q) buf[(p + PF) % NB][q] = x1_load<QT, DL>(rowbuf(i + PF, q), ul);
+      __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the math
       if (i < nrow) {
         float v[NR];
 #pragma unroll
-        for (int q = 0; q < NR; ++q) {
-          v[q] = wave_sum_dpp(x1_unit_dot<QT>(buf[p][q], lc, xa));
-        }
-        if (i + PF < nrow) {
-#pragma unroll
-          for (int q = 0; q < NR; ++q) buf[p][q] = x1_load<QT, DL>(rowbuf(i + PF, q), ul);
-        }
-        if (lane == 0) {
-          int mat = 0, lrow = w + i * W;
-          if constexpr (MODE == kPlain) row_of(job, lrow, mat, lrow);
-          if constexpr (MODE == kResid) {
-            const float out = job.resid[lrow] + v[0];
-            job.resid[lrow] = out;
-            if (job.resid_bf16) job.resid_bf16[lrow] = f32_to_bf16_rne(out);
-          } else {
-            float out = v[0];
-            if constexpr (MODE == kSwiGLU) out = silu(v[0]) * v[1];
-            if (MODE == kPlain && job.bias) out += job.bias[lrow];
-            if (job.y[mat]) job.y[mat][lrow] = out;
-            if (job.yb[mat]) job.yb[mat][lrow] = f32_to_bf16_rne(out);
-          }
-        }
+        for (int q = 0; q < NR; ++q) v[q] = wave_sum_dpp(x1_unit_dot<QT>(buf[p][q], lc, xa));
+        float out = v[0];
+        if constexpr (MODE == kSwiGLU) out = silu(v[0]) * v[1];
+        res = (lane == (i & 63)) ? out : res;
+        if ((i & 63) == 63) flush(i - 63, 64);
       }
     }
   }
+  if (nrow & 63) flush(nrow & ~63, nrow & 63);
 }
 
 template <int QT, bool DL, int MODE, int PF>
 static int launch_x1p(const StreamJob& job, int blocks_per_cu, hipStream_t s) {
-  const size_t lds = x1_lds_bytes(QT, job.k);
+  if (job.k > 4096 || job.k % 256 != 0) return set_error(DRACO_EINVAL_SHAPE, "persistent GEMV takes K <= 4096");
+  const size_t lds = x1p_lds_bytes(QT, job.k);
   const int need = (job.rows + 3) / 4;
   const int blocks = std::max(1, std::min(need, device_cus() * blocks_per_cu));
   hipLaunchKernelGGL((gemv_x1p_kernel<QT, DL, MODE, PF>), dim3(blocks), dim3(256), lds, s, job);

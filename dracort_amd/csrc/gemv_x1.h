@@ -191,17 +191,25 @@ __device__ __forceinline__ void x1_stage(uint4* lds, const uint16_t* __restrict_
   x1_stage_sums<QT>(lds, k);
 }
 
-// The same from chunks threadIdx.x and threadIdx.x + 256 already in
-// registers (workgroups of 256 threads, K <= 4096).  Chunks past K go to a
-// 4 KB pad after the image (x1p_lds_bytes) instead of being skipped: with an
-// unconditional store the loads stay where they were issued instead of being
-// sunk into a branch behind the weight loads.
-template <int QT>
-__device__ __forceinline__ void x1_stage_regs(uint4* lds, const uint4 (&xr)[2], int k) {
+// The same from XC chunks per thread already in registers (chunk
+// threadIdx.x + 256 j in xr[j]; workgroups of 256 threads, K <= 2048 XC).
+// Chunks past K go to a 4 KB pad after the image (x1p_lds_bytes) instead of
+// being skipped: with an unconditional store the loads stay where they were
+// issued instead of being sunk into a branch behind the weight loads.
+template <int XC>
+__device__ __forceinline__ void x1_fetch_x(const void* __restrict__ x, int k, uint4 (&xr)[XC]) {
+  const uint4* xs = static_cast<const uint4*>(x);
+  const int chunks = k >> 3;
+#pragma unroll
+  for (int j = 0; j < XC; ++j) xr[j] = xs[min((int)threadIdx.x + 256 * j, chunks - 1)];
+}
+
+template <int QT, int XC>
+__device__ __forceinline__ void x1_stage_regs(uint4* lds, const uint4 (&xr)[XC], int k) {
   const int chunks = k >> 3;
   const int pad = (int)(x1_lds_bytes(QT, k) / 16);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < XC; ++j) {
     const int c = (int)threadIdx.x + 256 * j;
     lds[c < chunks ? (c >> 9) * 512 + x1_slot_of_chunk<QT>(c & 511) : pad + (int)threadIdx.x] = xr[j];
   }
@@ -377,96 +385,67 @@ __global__ __launch_bounds__(256, OCC) void gemv_x1_kernel(StreamJob job) {
   }
 }
 
-// Persistent form for rows of one step (K <= 4096): a fixed grid of waves,
-// wave w computes rows w, w + W, w + 2W, ... (W = all waves) with the packed
-// bytes of the next PF rows in flight while it multiplies the current one.
-// Issue order keeps every vector-memory wait exact: the activations are
-// requested first, then the first PF rows; each iteration requests row i + PF
-// (through an empty buffer resource once past the wave's last row, so the
-// load instruction is always issued and returns zeros without touching
-// memory) before it multiplies row i; results are kept in lane i % 64 of one
-// register and stored after the loop, so no store sits between the loads.
-template <int QT, bool DL, int MODE, int PF>
-__global__ __launch_bounds__(256) void gemv_x1p_kernel(StreamJob job) {
-  constexpr int NR = MODE == kSwiGLU ? 2 : 1;
-  constexpr int NB = PF + 1;
-  extern __shared__ uint4 x1_smem[];
-  const int lane = threadIdx.x & 63;
-  const int W = gridDim.x * 4;
-  const int w = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nrow = job.rows > w ? (job.rows - w + W - 1) / W : 0;
-  const int k = job.k;
-  const int units = k >> 6;
-  const bool live = lane < units;
-  const int ul = live ? lane : units - 1;
-
-  // kPlain: up to four matrices with their rows concatenated; row r belongs
-  // to matrix (r >= c1) + (r >= c2) + (r >= c3)
+// Rows of a persistent wave: w, w + W, w + 2W, ... of the launch's row
+// space.  kPlain concatenates up to four matrices (row r belongs to matrix
+// (r >= c1) + (r >= c2) + (r >= c3)); kSwiGLU pairs gate and up.  Buffer
+// resources are built once; rows past the wave's last get an empty resource,
+// so their loads are issued (keeping every wait count exact) but return
+// zeros without touching memory.
+template <int MODE>
+struct X1Rows {
+  static constexpr int NR = MODE == kSwiGLU ? 2 : 1;
+  static constexpr int NM = MODE == kPlain ? kMaxMats : NR;
+  int w, W, nrow;
   int c1 = INT_MAX, c2 = INT_MAX, c3 = INT_MAX;
-  if constexpr (MODE == kPlain) {
-    if (job.n_mats > 1) c1 = job.n[0];
-    if (job.n_mats > 2) c2 = c1 + job.n[1];
-    if (job.n_mats > 3) c3 = c2 + job.n[2];
-  }
-  constexpr int NM = MODE == kPlain ? kMaxMats : NR;
   __amdgpu_buffer_rsrc_t rs[NM];
-#pragma unroll
-  for (int m = 0; m < NM; ++m)
-    rs[m] = make_rsrc(job.w[m], m < job.n_mats || NR == 2 ? (uint32_t)((int64_t)job.n[m] * job.row_bytes) : 0u);
-  const __amdgpu_buffer_rsrc_t empty = make_rsrc(job.w[0], 0u);
+  __amdgpu_buffer_rsrc_t empty;
 
-  auto rowbuf = [&](int i, int q) {
+  __device__ __forceinline__ X1Rows(const StreamJob& job) {
+    W = gridDim.x * 4;
+    w = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    nrow = job.rows > w ? (job.rows - w + W - 1) / W : 0;
+    if constexpr (MODE == kPlain) {
+      if (job.n_mats > 1) c1 = job.n[0];
+      if (job.n_mats > 2) c2 = c1 + job.n[1];
+      if (job.n_mats > 3) c3 = c2 + job.n[2];
+    }
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+      rs[m] = make_rsrc(job.w[m], m < job.n_mats || NR == 2 ? (uint32_t)((int64_t)job.n[m] * job.row_bytes) : 0u);
+    empty = make_rsrc(job.w[0], 0u);
+  }
+  __device__ __forceinline__ void locate(int r, int& mat, int& lrow) const {
+    mat = 0;
+    lrow = r;
+    if constexpr (MODE == kPlain) {
+      mat = (r >= c1) + (r >= c2) + (r >= c3);
+      lrow = r - (mat == 0 ? 0 : mat == 1 ? c1 : mat == 2 ? c2 : c3);
+    }
+  }
+  // wave-uniform: matrix q (kSwiGLU) / the owning matrix (kPlain) of row i
+  __device__ __forceinline__ X1Buf buf(const StreamJob& job, int i, int q) const {
     X1Buf b;
     if (i >= nrow) {
       b.rsrc = empty;
       b.soff = 0;
       return b;
     }
-    const int r = w + i * W;
+    int mat, lrow;
+    locate(w + i * W, mat, lrow);
     if constexpr (MODE == kPlain) {
-      const int mat = (r >= c1) + (r >= c2) + (r >= c3);
-      const int base = mat == 0 ? 0 : mat == 1 ? c1 : mat == 2 ? c2 : c3;
       b.rsrc = mat == 0 ? rs[0] : mat == 1 ? rs[1] : mat == 2 ? rs[2] : rs[3];
-      b.soff = (r - base) * job.row_bytes;
     } else {
       b.rsrc = rs[q];
-      b.soff = r * job.row_bytes;
     }
+    b.soff = lrow * job.row_bytes;
     return b;
-  };
-
-  // 1. activations (at most two 16-byte chunks per thread), then the first rows
-  uint4 xr[2];
-  {
-    const uint4* xs = static_cast<const uint4*>(job.x);
-    const int chunks = k >> 3;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) xr[j] = xs[min((int)threadIdx.x + 256 * j, chunks - 1)];
   }
-  X1Raw<QT> buf[NB][NR];
-#pragma unroll
-  for (int p = 0; p < PF; ++p)
-#pragma unroll
-    for (int q = 0; q < NR; ++q) buf[p][q] = x1_load<QT, DL>(rowbuf(p, q), ul);
-
-  // 2. the LDS image and group sums; the lane's activations into registers
-  x1_stage_regs<QT>(x1_smem, xr, k);
-  if (nrow == 0) return;
-  const X1Lane lc = x1_lane<QT>(lane);
-  X1Act xa;
-  x1_read_lds<QT>(x1_smem, k, 0, lane, live, xa);
-
-  // 3. rows
-  float res = 0.f;
-  auto flush = [&](int i0, int cnt) {
-    const int i = i0 + lane;
+  // lanes 0 .. cnt - 1 store the results of rows i0 + lane (held in res)
+  __device__ __forceinline__ void flush(const StreamJob& job, int i0, int cnt, float res) const {
+    const int lane = threadIdx.x & 63;
     if (lane >= cnt) return;
-    const int r = w + i * W;
-    int mat = 0, lrow = r;
-    if constexpr (MODE == kPlain) {
-      mat = (r >= c1) + (r >= c2) + (r >= c3);
-      lrow = r - (mat == 0 ? 0 : mat == 1 ? c1 : mat == 2 ? c2 : c3);
-    }
+    int mat, lrow;
+    locate(w + (i0 + lane) * W, mat, lrow);
     if constexpr (MODE == kResid) {
       const float out = job.resid[lrow] + res;
       job.resid[lrow] = out;
@@ -483,13 +462,54 @@ __global__ __launch_bounds__(256) void gemv_x1p_kernel(StreamJob job) {
       if (y) y[lrow] = out;
       if (yb) yb[lrow] = f32_to_bf16_rne(out);
     }
-  };
+  }
+};
+
+// Persistent form for rows of one step (K <= 4096): a fixed grid of waves,
+// wave w computes rows w, w + W, w + 2W, ... (W = all waves) with the packed
+// bytes of the next PF rows in flight while it multiplies the current one.
+// Issue order keeps every vector-memory wait exact: the activations are
+// requested first, then the first PF rows; each iteration requests row i + PF
+// before it multiplies row i; results are kept in lane i % 64 of one register
+// and stored after every 64 rows, so no store sits between the loads.  The
+// activations (the bf16 LDS image) are read into registers once.
+template <int QT, bool DL, int MODE, int PF>
+__global__ __launch_bounds__(256) void gemv_x1p_kernel(StreamJob job) {
+  constexpr int NR = MODE == kSwiGLU ? 2 : 1;
+  constexpr int NB = PF + 1;
+  extern __shared__ uint4 x1_smem[];
+  const int lane = threadIdx.x & 63;
+  const X1Rows<MODE> rows(job);
+  const int nrow = rows.nrow;
+  const int k = job.k;
+  const int units = k >> 6;
+  const bool live = lane < units;
+  const int ul = live ? lane : units - 1;
+
+  // 1. activations (two 16-byte chunks per thread), then the first rows
+  uint4 xr[2];
+  x1_fetch_x<2>(job.x, k, xr);
+  X1Raw<QT> buf[NB][NR];
+#pragma unroll
+  for (int p = 0; p < PF; ++p)
+#pragma unroll
+    for (int q = 0; q < NR; ++q) buf[p][q] = x1_load<QT, DL>(rows.buf(job, p, q), ul);
+
+  // 2. the LDS image and group sums; the lane's activations into registers
+  x1_stage_regs<QT, 2>(x1_smem, xr, k);
+  if (nrow == 0) return;
+  const X1Lane lc = x1_lane<QT>(lane);
+  X1Act xa;
+  x1_read_lds<QT>(x1_smem, k, 0, lane, live, xa);
+
+  // 3. rows
+  float res = 0.f;
   for (int i0 = 0; i0 < nrow; i0 += NB) {
 #pragma unroll
     for (int p = 0; p < NB; ++p) {
       const int i = i0 + p;
 #pragma unroll
-      for (int q = 0; q < NR; ++q) buf[(p + PF) % NB][q] = x1_load<QT, DL>(rowbuf(i + PF, q), ul);
+      for (int q = 0; q < NR; ++q) buf[(p + PF) % NB][q] = x1_load<QT, DL>(rows.buf(job, i + PF, q), ul);
       __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the math
       if (i < nrow) {
         float v[NR];
@@ -498,11 +518,11 @@ __global__ __launch_bounds__(256) void gemv_x1p_kernel(StreamJob job) {
         float out = v[0];
         if constexpr (MODE == kSwiGLU) out = silu(v[0]) * v[1];
         res = (lane == (i & 63)) ? out : res;
-        if ((i & 63) == 63) flush(i - 63, 64);
+        if ((i & 63) == 63) rows.flush(job, i - 63, 64, res);
       }
     }
   }
-  if (nrow & 63) flush(nrow & ~63, nrow & 63);
+  if (nrow & 63) rows.flush(job, nrow & ~63, nrow & 63, res);
 }
 
 template <int QT, bool DL, int MODE, int PF>
@@ -691,10 +711,12 @@ static int gemv_dispatch_mode(int qtype, bool d_last, const StreamJob& job, bool
   for (int i = 0; i < job.n_mats; ++i)
     if ((int64_t)job.n[i] * job.row_bytes >= ((int64_t)1 << 31)) x1 = false;  // 32-bit buffer offsets
   if (x1 && job.k <= 4096) {
-    constexpr int kBlocksPerCu = 4;
-    if (qtype == kQ4_K) return launch_x1p<kQ4_K, false, MODE, 2>(job, kBlocksPerCu, s);
-    return d_last ? launch_x1p<kQ6_K, true, MODE, 2>(job, kBlocksPerCu, s)
-                  : launch_x1p<kQ6_K, false, MODE, 2>(job, kBlocksPerCu, s);
+    // one row in flight ahead of the math; four workgroups per CU for long
+    // matrices, three below 8192 rows (measured: 14336 x 4096 Q4_K 8.6 us at
+    // four, 4096 x 4096 5.5 us at three vs 5.8 at four)
+    const int bpc = job.rows >= 8192 ? 4 : 3;
+    if (qtype == kQ4_K) return launch_x1p<kQ4_K, false, MODE, 1>(job, bpc, s);
+    return d_last ? launch_x1p<kQ6_K, true, MODE, 1>(job, bpc, s) : launch_x1p<kQ6_K, false, MODE, 1>(job, bpc, s);
   }
   // 8..16 activation rows: the matrix-core kernel (measured faster than the
   // streaming kernel from 8 rows on; at 4 rows they tie or the latter wins)

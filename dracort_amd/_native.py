@@ -29,7 +29,7 @@ DRACO_DTYPE_F32 = 0
 DRACO_DTYPE_BF16 = 1
 DRACO_GGUF_Q6K_D_LAST = 0x100
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _c_int, _c_i64, _c_size, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
 
@@ -47,8 +47,11 @@ SIGNATURES = {
     ),
     "draco_gguf_gemv_swiglu": (_c_int, [_c_int, _vp, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "draco_gguf_gemv_residual": (_c_int, [_c_int, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
-    "draco_gguf_gemm": (_c_int, [_c_int, _vp, _c_size, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
-    "draco_gguf_linear": (_c_int, [_c_int, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
+    "draco_gguf_gemm_workspace_size": (_c_size, [_c_int, _c_i64, _c_i64]),
+    "draco_gguf_gemm": (_c_int, [_c_int, _vp, _c_size, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_size, _vp]),
+    "draco_gguf_linear": (
+        _c_int, [_c_int, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_size, _vp]
+    ),
     "draco_gguf_moe_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "draco_gguf_moe_ffn": (
         _c_int,

@@ -96,7 +96,7 @@ using namespace draco;
 
 extern "C" {
 
-int draco_gguf_abi_version(void) { return 2; }
+int draco_gguf_abi_version(void) { return 3; }
 
 const char* draco_gguf_last_error(void) { return g_last_error; }
 
@@ -224,8 +224,14 @@ int draco_gguf_gemv_residual(int ggml_type, const void* w, size_t w_bytes, const
                              static_cast<hipStream_t>(stream));
 }
 
+size_t draco_gguf_gemm_workspace_size(int ggml_type, int64_t m, int64_t k) {
+  TypeInfo t;
+  if (decode_type(ggml_type, &t) || m < 1 || k < 1) return 0;
+  return gemm_workspace_size(t.base, m, k);
+}
+
 int draco_gguf_gemm(int ggml_type, const void* w, size_t w_bytes, const void* x_bf16, const float* bias, float* y,
-                    int64_t m, int64_t n, int64_t k, void* stream) {
+                    int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes, void* stream) {
   g_last_error[0] = 0;
   TypeInfo t;
   if (int rc = decode_type(ggml_type, &t)) return rc;
@@ -235,14 +241,23 @@ int draco_gguf_gemm(int ggml_type, const void* w, size_t w_bytes, const void* x_
   if (int rc = check_ptr(w, "w")) return rc;
   if (int rc = check_ptr(x_bf16, "x")) return rc;
   if (int rc = check_ptr(y, "y")) return rc;
-  return gemm_dispatch(t.base, t.d_last, w, x_bf16, bias, y, (int)m, (int)n, (int)k,
+  if (workspace) {
+    const size_t need = gemm_workspace_size(t.base, m, k);
+    if (workspace_bytes < need)
+      return set_error(DRACO_EWORKSPACE, "GEMM workspace needs %zu bytes, got %zu", need, workspace_bytes);
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+      return set_error(DRACO_EINVAL_ARG, "GEMM workspace must be 256-byte aligned");
+  }
+  return gemm_dispatch(t.base, t.d_last, w, x_bf16, bias, y, (int)m, (int)n, (int)k, workspace,
                        static_cast<hipStream_t>(stream));
 }
 
 int draco_gguf_linear(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype, const float* bias,
-                      float* y, int64_t m, int64_t n, int64_t k, void* stream) {
+                      float* y, int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
+                      void* stream) {
   if (m >= 1 && m <= 16) return draco_gguf_gemv(ggml_type, w, w_bytes, x, x_dtype, bias, y, m, n, k, stream);
-  if (x_dtype == DRACO_DTYPE_BF16) return draco_gguf_gemm(ggml_type, w, w_bytes, x, bias, y, m, n, k, stream);
+  if (x_dtype == DRACO_DTYPE_BF16)
+    return draco_gguf_gemm(ggml_type, w, w_bytes, x, bias, y, m, n, k, workspace, workspace_bytes, stream);
   g_last_error[0] = 0;
   if (m < 1 || m > kMaxDim) return set_error(DRACO_EINVAL_SHAPE, "invalid token count %lld", (long long)m);
   if (x_dtype != DRACO_DTYPE_F32) return set_error(DRACO_EINVAL_ARG, "unknown activation dtype %d", x_dtype);

@@ -31,7 +31,11 @@ int gemv_swiglu_dispatch(int qtype, bool d_last, const void* w_gate, const void*
 int gemv_resid_dispatch(int qtype, bool d_last, const void* w, const void* x, bool xbf16, float* resid,
                         uint16_t* resid_bf16, int m, int n, int k, hipStream_t s);
 
+// Workspace bytes of the GEMM of this base type (0: it needs none).
+size_t gemm_workspace_size(int qtype, int64_t m, int64_t k);
+
+// workspace: NULL, or gemm_workspace_size(qtype, m, k) bytes, 256-byte aligned.
 int gemm_dispatch(int qtype, bool d_last, const void* w, const void* x_bf16, const float* bias, float* y,
-                  int m, int n, int k, hipStream_t s);
+                  int m, int n, int k, void* workspace, hipStream_t s);
 
 }  // namespace draco

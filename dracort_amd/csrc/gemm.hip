@@ -21,6 +21,7 @@
 // The next K step's global loads are issued before the MFMAs of the current
 // one so that HBM latency overlaps the matrix work.
 #include "draco_internal.h"
+#include "gemm_q4k.h"
 #include "gemv_core.h"
 
 namespace draco {
@@ -209,8 +210,17 @@ static int launch_gemm(const void* w, const void* x, const float* bias, float* y
   return check_launch("gemm");
 }
 
+size_t gemm_workspace_size(int qtype, int64_t m, int64_t k) {
+  return qtype == kQ4_K ? gemm_q4k_ws_layout(m, k, nullptr, nullptr) : 0;
+}
+
 int gemm_dispatch(int qtype, bool d_last, const void* w, const void* x, const float* bias, float* y, int m, int n,
-                  int k, hipStream_t s) {
+                  int k, void* workspace, hipStream_t s) {
+  if (qtype == kQ4_K && workspace) {
+    if ((int64_t)n * (k / 256) * 144 >= ((int64_t)1 << 31))
+      return set_error(DRACO_EINVAL_SHAPE, "Q4_K GEMM weight above 2 GiB");
+    return launch_gemm_q4k(w, x, bias, y, m, n, k, workspace, s);
+  }
   switch (qtype) {
     case kQ8_0: return launch_gemm<kQ8_0, false>(w, x, bias, y, m, n, k, s);
     case kQ4_0: return launch_gemm<kQ4_0, false>(w, x, bias, y, m, n, k, s);

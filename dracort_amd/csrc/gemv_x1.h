@@ -154,7 +154,7 @@ __host__ __device__ inline size_t x1_lds_bytes(int qtype, int k) {
 }
 
 // the persistent kernel's LDS: the image, its sums and a 4 KB pad
-inline size_t x1p_lds_bytes(int qtype, int k) { return x1_lds_bytes(qtype, k) + 256 * 16; }
+__host__ __device__ inline size_t x1p_lds_bytes(int qtype, int k) { return x1_lds_bytes(qtype, k) + 256 * 16; }
 
 // Group sums of the staged image (after the barrier that ends the stores);
 // ends in a barrier.

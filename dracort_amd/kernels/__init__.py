@@ -2,6 +2,7 @@
 
 from dracort_amd.kernels.gguf import (  # noqa: F401
     block_layout,
+    gemm_workspace_bytes,
     gguf_dequantize,
     gguf_gemm,
     gguf_gemv,
@@ -23,5 +24,6 @@ __all__ = [
     "gguf_gemm",
     "gguf_moe",
     "moe_workspace_bytes",
+    "gemm_workspace_bytes",
     "block_layout",
 ]

@@ -124,6 +124,23 @@ def _prep_linear(x, qweight, ggml_type, shape, bias, out):
     return m, n, k, xd, out
 
 
+def gemm_workspace_bytes(ggml_type: int, m: int, k: int) -> int:
+    """Device workspace bytes the prefill GEMM uses for ``m`` rows of length ``k``."""
+    return int(_native.load().draco_gguf_gemm_workspace_size(int(ggml_type), int(m), int(k)))
+
+
+def _gemm_workspace(ggml_type, m, k, device, workspace):
+    need = gemm_workspace_bytes(ggml_type, m, k)
+    if need == 0:
+        return None, 0
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    _need_gpu(workspace, "workspace")
+    if workspace.dtype != torch.uint8 or workspace.numel() < need:
+        raise ValueError(f"workspace must be uint8 with at least {need} bytes")
+    return workspace, workspace.numel()
+
+
 def gguf_linear(
     x: torch.Tensor,
     qweight: torch.Tensor,
@@ -131,14 +148,22 @@ def gguf_linear(
     shape: Tuple[int, int],
     bias: Optional[torch.Tensor] = None,
     out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """``x @ dequant(W).T (+ bias)`` for x [..., K] (float32 or bfloat16) -> float32 [..., N]."""
+    """``x @ dequant(W).T (+ bias)`` for x [..., K] (float32 or bfloat16) -> float32 [..., N].
+
+    Prompt-sized bfloat16 inputs take the prefill GEMM, with ``workspace``
+    (allocated here when not given) for the types whose GEMM uses one."""
     m, n, k, xd, out = _prep_linear(x, qweight, ggml_type, shape, bias, out)
+    ws, ws_bytes = (None, 0)
+    if m > GEMV_MAX_M and x.dtype == torch.bfloat16:
+        ws, ws_bytes = _gemm_workspace(ggml_type, m, k, x.device, workspace)
     lib = _native.load()
     with torch.cuda.device(x.device):
         rc = lib.draco_gguf_linear(
             int(ggml_type), qweight.data_ptr(), qweight.numel(), x.data_ptr(), xd,
-            bias.data_ptr() if bias is not None else None, out.data_ptr(), m, n, k, _stream(x),
+            bias.data_ptr() if bias is not None else None, out.data_ptr(), m, n, k,
+            ws.data_ptr() if ws is not None else None, ws_bytes, _stream(x),
         )
     _native.check(rc, "gguf_linear")
     return out
@@ -159,16 +184,20 @@ def gguf_gemv(x, qweight, ggml_type, shape, bias=None, out=None) -> torch.Tensor
     return out
 
 
-def gguf_gemm(x, qweight, ggml_type, shape, bias=None, out=None) -> torch.Tensor:
-    """Prefill GEMM (bf16 activations, MFMA), dequantization fused."""
+def gguf_gemm(x, qweight, ggml_type, shape, bias=None, out=None, workspace=None) -> torch.Tensor:
+    """Prefill GEMM (bf16 activations, MFMA), dequantization fused.  ``workspace``
+    (uint8 device tensor of ``gemm_workspace_bytes`` bytes) is allocated here
+    when not given."""
     if x.dtype != torch.bfloat16:
         raise ValueError(f"gguf_gemm takes bfloat16 activations, got {x.dtype}")
     m, n, k, xd, out = _prep_linear(x, qweight, ggml_type, shape, bias, out)
+    ws, ws_bytes = _gemm_workspace(ggml_type, m, k, x.device, workspace)
     lib = _native.load()
     with torch.cuda.device(x.device):
         rc = lib.draco_gguf_gemm(
             int(ggml_type), qweight.data_ptr(), qweight.numel(), x.data_ptr(),
-            bias.data_ptr() if bias is not None else None, out.data_ptr(), m, n, k, _stream(x),
+            bias.data_ptr() if bias is not None else None, out.data_ptr(), m, n, k,
+            ws.data_ptr() if ws is not None else None, ws_bytes, _stream(x),
         )
     _native.check(rc, "gguf_gemm")
     return out

@@ -123,21 +123,35 @@ int draco_gguf_gemv_residual(int ggml_type, const void* w, size_t w_bytes, const
                              void* resid_bf16, int64_t m, int64_t n, int64_t k, void* stream);
 
 /*
- * Prefill GEMM with the dequantization fused in (weight tiles decoded into
- * LDS, bf16 MFMA, float32 accumulate and output):
- *   y[m, n] = x_bf16[m, k] . W[n, k]^T (+ bias[n]),  m >= 1.
- * Same reference call sites as draco_gguf_gemv, for prompt-sized M.
+ * Workspace bytes draco_gguf_gemm / draco_gguf_linear use for m token rows of
+ * length k with this weight type (0 when the type's GEMM needs none).  Q4_K
+ * takes m * k * 2 + 3 * m * (k / 32) * 2 + m * 4 bytes (rounded up to 256 per
+ * part): the activations as float16 and their 32-element sums.
  */
-int draco_gguf_gemm(int ggml_type, const void* w, size_t w_bytes, const void* x_bf16, const float* bias, float* y,
-                    int64_t m, int64_t n, int64_t k, void* stream);
+size_t draco_gguf_gemm_workspace_size(int ggml_type, int64_t m, int64_t k);
 
 /*
- * _linear for any M: draco_gguf_gemv for m <= 16, draco_gguf_gemm for larger
- * m with bf16 activations, and 16-row GEMV tiles for larger m with float32
- * activations.  Replaces _linear (draco/runtime/cpu/executor.py:47-79).
+ * Prefill GEMM with the dequantization fused in (bf16 activations, MFMA,
+ * float32 accumulate and output):
+ *   y[m, n] = x_bf16[m, k] . W[n, k]^T (+ bias[n]),  m >= 1.
+ * Same reference call sites as draco_gguf_gemv, for prompt-sized M.
+ * `workspace` (device memory, workspace_bytes >= draco_gguf_gemm_workspace_size)
+ * selects the float16 matrix-core kernel for Q4_K; NULL runs the
+ * workspace-free kernel (three bf16 weight planes, slower).  A workspace that
+ * is given but too small is an error (DRACO_EWORKSPACE).
+ */
+int draco_gguf_gemm(int ggml_type, const void* w, size_t w_bytes, const void* x_bf16, const float* bias, float* y,
+                    int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * _linear for any M: draco_gguf_gemv for m <= 16, draco_gguf_gemm (with the
+ * workspace, which may be NULL) for larger m with bf16 activations, and
+ * 16-row GEMV tiles for larger m with float32 activations.  Replaces _linear
+ * (draco/runtime/cpu/executor.py:47-79).
  */
 int draco_gguf_linear(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype, const float* bias,
-                      float* y, int64_t m, int64_t n, int64_t k, void* stream);
+                      float* y, int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
+                      void* stream);
 
 /*
  * Workspace bytes draco_gguf_moe_ffn needs for `tokens` tokens.

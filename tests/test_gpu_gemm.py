@@ -5,7 +5,8 @@ import numpy as np
 import pytest
 import torch
 
-from dracort_amd.kernels import gguf_gemm, gguf_linear
+from dracort_amd import _native
+from dracort_amd.kernels import gemm_workspace_bytes, gguf_gemm, gguf_linear
 from oracle import matmul_ref
 from tests.gguf_cases import NAMES, Q4_K, Q6_K, Q8_0, TYPES, activations, check_close, quantized
 
@@ -48,3 +49,48 @@ def test_gemm_via_linear_dispatch_and_bias():
 def test_gemm_q8_0_k_not_multiple_of_64():
     y, ref = _run(Q8_0, 96, 96, 70, seed=8)
     check_close(y, ref, "gemm Q8_0 K=96")
+
+
+def test_gemm_q4k_large_activations_row_scaling():
+    """Rows whose largest |x| is beyond float16's range are scaled by a power
+    of two for the float16 matrix cores and unscaled on the output."""
+    blocks, w = quantized(Q4_K, 256, 1024, 11)
+    x = activations(70, 1024, 11, torch.float32)
+    x[3, 5] = 1.5e5
+    x[17, 900] = -7.0e6
+    x[40] *= 3.0e4  # a whole row far beyond 65504
+    x = x.to(torch.bfloat16)
+    print("gemm Q4_K large activations", flush=True)
+    y = gguf_gemm(x.cuda(), torch.from_numpy(blocks).cuda(), Q4_K, (256, 1024)).cpu().numpy()
+    ref = matmul_ref.linear_ref(x.float().numpy(), w)
+    for r in (3, 17, 40, 0, 69):
+        check_close(y[r], ref[r], f"gemm Q4_K large x row {r}")
+
+
+def test_gemm_q4k_without_workspace_matches():
+    """A NULL workspace runs the workspace-free kernel; both agree with the oracle."""
+    n, k, m = 384, 1024, 200
+    blocks, w = quantized(Q4_K, n, k, 12)
+    x = activations(m, k, 12, torch.bfloat16).cuda()
+    wq = torch.from_numpy(blocks).cuda()
+    y0 = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    lib = _native.load()
+    print("gemm Q4_K workspace-free", flush=True)
+    rc = lib.draco_gguf_gemm(Q4_K, wq.data_ptr(), wq.numel(), x.data_ptr(), None, y0.data_ptr(), m, n, k, None, 0,
+                             torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _native.last_error()
+    y1 = gguf_gemm(x, wq, Q4_K, (n, k))
+    ref = matmul_ref.linear_ref(x.cpu().float().numpy(), w)
+    check_close(y0.cpu().numpy(), ref, "gemm Q4_K no workspace")
+    check_close(y1.cpu().numpy(), ref, "gemm Q4_K workspace")
+    assert gemm_workspace_bytes(Q4_K, m, k) > 0
+
+
+def test_gemm_q4k_m2048_bias_via_linear():
+    blocks, w = quantized(Q4_K, 1024, 2048, 13)
+    x = activations(2048, 2048, 13, torch.bfloat16)
+    b = torch.from_numpy(np.random.default_rng(13).standard_normal(1024, dtype=np.float32))
+    print("linear Q4_K m=2048 bias", flush=True)
+    y = gguf_linear(x.cuda(), torch.from_numpy(blocks).cuda(), Q4_K, (1024, 2048), bias=b.cuda()).cpu().numpy()
+    ref = matmul_ref.linear_ref(x.float().numpy(), w) + b.numpy()
+    check_close(y, ref, "linear Q4_K m=2048")

@@ -71,7 +71,16 @@ def test_error_codes_before_launch():
     assert gemv(12, FAKE, 1 << 20, FAKE, 1, None, FAKE, 17, 4, 256, None) == _native.DRACO_EINVAL_SHAPE  # M > 16
     assert gemv(12, FAKE, 1 << 20, FAKE, 1, None, FAKE, 0, 4, 256, None) == _native.DRACO_EINVAL_SHAPE
     assert gemv(12, FAKE, 1 << 20, FAKE, 7, None, FAKE, 1, 4, 256, None) == _native.DRACO_EINVAL_ARG    # dtype
-    assert lib.draco_gguf_gemm(8, FAKE, 10, FAKE, None, FAKE, 64, 4, 64, None) == _native.DRACO_EINVAL_SHAPE
+    assert lib.draco_gguf_gemm(8, FAKE, 10, FAKE, None, FAKE, 64, 4, 64, None, 0, None) == _native.DRACO_EINVAL_SHAPE
+    # prefill GEMM workspace: Q4_K needs f16 activations + three planes of 32-element sums + row scales
+    al = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    need = al(512 * 4096 * 2) + al(3 * 512 * 128 * 2) + al(512 * 4)
+    assert lib.draco_gguf_gemm_workspace_size(12, 512, 4096) == need
+    assert lib.draco_gguf_gemm_workspace_size(8, 512, 4096) == 0
+    assert lib.draco_gguf_gemm_workspace_size(99, 512, 4096) == 0
+    gemm = lib.draco_gguf_gemm
+    assert gemm(12, FAKE, 1 << 30, FAKE, None, FAKE, 512, 64, 4096, FAKE, need - 1, None) == _native.DRACO_EWORKSPACE
+    assert gemm(12, FAKE, 1 << 30, FAKE, None, FAKE, 512, 64, 4096, FAKE + 16, need, None) == _native.DRACO_EINVAL_ARG
     ptrs = (ctypes.c_void_p * 2)(FAKE, FAKE)
     moe = lib.draco_gguf_moe_ffn
     args = [12, ptrs, ptrs, ptrs, 1 << 30, FAKE, FAKE, 1, FAKE, 64, 256, 512, 2, 2, FAKE, 1 << 30, None]

@@ -7,3 +7,4 @@ from dracort_amd.runtime.decode import (  # noqa: F401
     layer_set_bytes,
     synthetic_layer_set,
 )
+from dracort_amd.runtime.gpu_tier import GGUFGpuKernel, is_gguf_block_tensor  # noqa: F401

@@ -185,3 +185,18 @@ def test_registry_has_gguf_backend():
     assert info["gpu_kernel"] and info["arch"] == "gfx950"
     assert be.supports_gpu_kernel(torch.device("cuda"))
     assert be.estimate_memory(4096 * 4096, 4) == 4096 * 4096 * 9 // 16
+
+
+def test_gpu_tier_selection_rules():
+    from dracort_amd.format.gguf import GgufTensorInfo
+    from dracort_amd.runtime import GGUFGpuKernel, is_gguf_block_tensor
+
+    k = GGUFGpuKernel()
+    assert k.tier == "gpu-gguf" and k.name == "mi355x-gguf"
+    assert k.supports(None) and not k.supports("int8_sym")
+    assert is_gguf_block_tensor(GgufTensorInfo("w", 12, (16, 256)))
+    assert is_gguf_block_tensor(GgufTensorInfo("w", 14 | 0x100, (16, 256)))
+    assert not is_gguf_block_tensor(GgufTensorInfo("w", 0, (16, 256)))          # float32
+    assert not is_gguf_block_tensor(GgufTensorInfo("w", 3, (16, 256)))          # Q4_1: no kernel here
+    assert not is_gguf_block_tensor(GgufTensorInfo("w", 12, (4096,)))           # not 2-D
+    assert not is_gguf_block_tensor(GgufTensorInfo("w", 12, (16, 256), quantization="int8_sym"))

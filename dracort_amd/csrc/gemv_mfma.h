@@ -248,7 +248,106 @@ __device__ __forceinline__ void mf_accumulate(const __amdgpu_buffer_rsrc_t (&rs)
 
 }
 
-template <int QT, bool XBF16, int MODE, int TPW>
+// Q6_K: sixteen 16-weight groups per 256-weight chunk, each with its own int8
+// scale, so one v_mfma_f32_16x16x16_bf16 per group (lane l: row / column
+// l % 16, k slice 4 (l / 16)).  A lane's codes of group g = 8n + 2t + h
+// (half n, shift t, sixteen-element half h) are bytes 16h + 4q .. + 4 of
+// ql[64n + 32 (t & 1)] (nibble t >> 1) and of qh[32n] (bits 2t, 2t + 1):
+// eight ql dwords and four qh dwords per lane and chunk, 2-byte aligned
+// (unaligned loads).  With B = 128 + q exact in bf16 and w = d sc_g (q - 32),
+// sum_k x w = d sc_g (D - 160 S) per group.
+typedef short mf_s16x4 __attribute__((ext_vector_type(4)));
+struct MfQ6 {
+  uint32_t ql[8];  // [4n + 2 (t & 1) + h]
+  uint32_t qh[4];  // [2n + h]
+  uint4 sc;        // the 16 int8 group scales
+  uint32_t d;
+};
+
+template <bool DL>
+__device__ __forceinline__ MfQ6 mf_load_q6(__amdgpu_buffer_rsrc_t rsrc, int rowoff, int chunk, int q) {
+  constexpr int QL = DL ? 0 : 2, QH = DL ? 128 : 130, SC = DL ? 192 : 194, D = DL ? 208 : 0;
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  const int base = rowoff + chunk * 210;
+  MfQ6 c;
+#pragma unroll
+  for (int n = 0; n < 2; ++n)
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        c.ql[4 * n + 2 * tb + h] =
+            (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsrc, base + QL + 64 * n + 32 * tb + 16 * h + 4 * q, 0, 0);
+#pragma unroll
+  for (int n = 0; n < 2; ++n)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      c.qh[2 * n + h] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsrc, base + QH + 32 * n + 16 * h + 4 * q, 0, 0);
+  const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, base + SC, 0, 0);
+  c.sc = uint4{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+  c.d = (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rsrc, base + D, 0, 0);
+  return c;
+}
+
+// B operand of group g: 4 codes as bf16 128 + q.
+__device__ __forceinline__ mf_s16x4 mf_codes_q6(const MfQ6& c, int g) {
+  const int n = g >> 3, t = (g >> 1) & 3, h = g & 1;
+  const uint32_t lo = (c.ql[4 * n + 2 * (t & 1) + h] >> (4 * (t >> 1))) & 0x0F0F0F0Fu;
+  const uint32_t hi = ((c.qh[2 * n + h] >> (2 * t)) & 0x03030303u) << 4;
+  const uint32_t q = lo | hi;
+  const uint32_t v[2] = {__builtin_amdgcn_perm(0x43434343u, q, 0x04010400u),
+                         __builtin_amdgcn_perm(0x43434343u, q, 0x04030402u)};
+  return __builtin_bit_cast(mf_s16x4, v);
+}
+
+template <bool DL, int NR>
+__device__ __forceinline__ void mf_accumulate_q6k(const __amdgpu_buffer_rsrc_t (&rs)[NR], int rowoff,
+                                                  const void* __restrict__ xrow, int q, int ks, int chunks,
+                                                  mf_f32x4 (&acc)[NR]) {
+  const uint32_t ones2[2] = {kOnePair, kOnePair};
+  const mf_s16x4 bones = __builtin_bit_cast(mf_s16x4, ones2);
+  const uint16_t* x = static_cast<const uint16_t*>(xrow);
+  MfQ6 wb[2][NR];
+  uint2 xb[2][16];
+  auto load_chunk = [&](int slot, int cc) {
+#pragma unroll
+    for (int g = 0; g < 16; ++g) xb[slot][g] = *reinterpret_cast<const uint2*>(x + cc * 256 + 16 * g + 4 * q);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) wb[slot][r] = mf_load_q6<DL>(rs[r], rowoff, cc, q);
+  };
+  auto compute_chunk = [&](int slot) {
+    float a[NR][16];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const float d = f16_bits_to_f32(wb[slot][r].d);
+      const uint32_t sw[4] = {wb[slot][r].sc.x, wb[slot][r].sc.y, wb[slot][r].sc.z, wb[slot][r].sc.w};
+#pragma unroll
+      for (int g = 0; g < 16; ++g) a[r][g] = d * sbyte_f(sw[g >> 2], g & 3);
+    }
+    const mf_f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      const mf_s16x4 av = __builtin_bit_cast(mf_s16x4, xb[slot][g]);
+      const mf_f32x4 sg = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bones, z, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const mf_f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, mf_codes_q6(wb[slot][r], g), z, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[r][v] = fmaf(a[r][g], fmaf(-(kCodeBias + 32.f), sg[v], dg[v]), acc[r][v]);
+      }
+    }
+  };
+  if (ks < chunks) load_chunk(0, ks);
+  for (int c = ks; c < chunks; c += 8) {
+    if (c + 4 < chunks) load_chunk(1, c + 4);
+    compute_chunk(0);
+    if (c + 4 >= chunks) break;
+    if (c + 8 < chunks) load_chunk(0, c + 8);
+    compute_chunk(1);
+  }
+}
+
+template <int QT, bool DL, bool XBF16, int MODE, int TPW>
 __global__ __launch_bounds__(TPW * 256) void gemv_mfma_kernel(StreamJob job) {
   constexpr int NR = MODE == kSwiGLU ? 2 : 1;
   __shared__ mf_f32x4 part[TPW][4][NR][64];
@@ -280,7 +379,10 @@ __global__ __launch_bounds__(TPW * 256) void gemv_mfma_kernel(StreamJob job) {
 #pragma unroll
   for (int r = 0; r < NR; ++r) acc[r] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
   const void* xrow = static_cast<const uint8_t*>(job.x) + (size_t)min(nl, M - 1) * k * (XBF16 ? 2 : 4);
-  mf_accumulate<QT, XBF16, NR>(rs, rowoff, xrow, q, ks, chunks, acc);
+  if constexpr (QT == kQ6_K)
+    mf_accumulate_q6k<DL, NR>(rs, rowoff, xrow, q, ks, chunks, acc);
+  else
+    mf_accumulate<QT, XBF16, NR>(rs, rowoff, xrow, q, ks, chunks, acc);
 
   // sum the four K-split partial tiles
 #pragma unroll
@@ -325,8 +427,10 @@ __global__ __launch_bounds__(TPW * 256) void gemv_mfma_kernel(StreamJob job) {
 // Whether the matrix-core GEMV takes this launch: K-quant Q4_K or Q4_0,
 // 2..16 activation rows, K a multiple of 256, every matrix a whole number of
 // 16-row tiles, 32-bit buffer offsets.
-inline bool mfma_gemv_ok(int qtype, const StreamJob& job) {
-  if (!(qtype == kQ4_K || qtype == kQ4_0) || job.m < 2 || job.m > 16 || job.k % 256 != 0) return false;
+inline bool mfma_gemv_ok(int qtype, const StreamJob& job, bool xbf16) {
+  if (!(qtype == kQ4_K || qtype == kQ4_0 || (qtype == kQ6_K && xbf16)) || job.m < 2 || job.m > 16 ||
+      job.k % 256 != 0)
+    return false;
   for (int i = 0; i < job.n_mats; ++i) {
     if (job.n[i] % 16 != 0) return false;
     if ((int64_t)job.n[i] * job.row_bytes >= ((int64_t)1 << 31)) return false;
@@ -334,22 +438,27 @@ inline bool mfma_gemv_ok(int qtype, const StreamJob& job) {
   return true;
 }
 
-template <int QT, bool XBF16, int MODE>
+template <int QT, bool DL, bool XBF16, int MODE>
 static int launch_gemv_mfma(const StreamJob& job, hipStream_t s) {
   const int tiles = (job.rows + 15) / 16;
-  if (tiles >= 2048) {
-    hipLaunchKernelGGL((gemv_mfma_kernel<QT, XBF16, MODE, 2>), dim3((tiles + 1) / 2), dim3(512), 0, s, job);
+  // two tiles per workgroup for very tall matrices (bf16 only: with float32
+  // activations the 512-thread form would spill registers)
+  if (XBF16 && tiles >= 2048) {
+    hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 2>), dim3((tiles + 1) / 2), dim3(512), 0, s, job);
   } else {
-    hipLaunchKernelGGL((gemv_mfma_kernel<QT, XBF16, MODE, 1>), dim3(tiles), dim3(256), 0, s, job);
+    hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 1>), dim3(tiles), dim3(256), 0, s, job);
   }
   return check_launch("gemv_mfma");
 }
 
 template <int MODE>
-static int gemv_mfma_dispatch(int qtype, const StreamJob& job, bool xbf16, hipStream_t s) {
+static int gemv_mfma_dispatch(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s) {
+  if (qtype == kQ6_K)
+    return d_last ? launch_gemv_mfma<kQ6_K, true, true, MODE>(job, s) : launch_gemv_mfma<kQ6_K, false, true, MODE>(job, s);
   if (qtype == kQ4_K)
-    return xbf16 ? launch_gemv_mfma<kQ4_K, true, MODE>(job, s) : launch_gemv_mfma<kQ4_K, false, MODE>(job, s);
-  return xbf16 ? launch_gemv_mfma<kQ4_0, true, MODE>(job, s) : launch_gemv_mfma<kQ4_0, false, MODE>(job, s);
+    return xbf16 ? launch_gemv_mfma<kQ4_K, false, true, MODE>(job, s)
+                 : launch_gemv_mfma<kQ4_K, false, false, MODE>(job, s);
+  return xbf16 ? launch_gemv_mfma<kQ4_0, false, true, MODE>(job, s) : launch_gemv_mfma<kQ4_0, false, false, MODE>(job, s);
 }
 
 }  // namespace draco

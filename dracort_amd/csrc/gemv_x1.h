@@ -720,7 +720,7 @@ static int gemv_dispatch_mode(int qtype, bool d_last, const StreamJob& job, bool
   }
   // 8..16 activation rows: the matrix-core kernel (measured faster than the
   // streaming kernel from 8 rows on; at 4 rows they tie or the latter wins)
-  if (job.m >= 8 && mfma_gemv_ok(qtype, job)) return gemv_mfma_dispatch<MODE>(qtype, job, xbf16, s);
+  if (job.m >= 8 && mfma_gemv_ok(qtype, job, xbf16)) return gemv_mfma_dispatch<MODE>(qtype, d_last, job, xbf16, s);
   if constexpr (MODE != kSwiGLU) {
     if (x1 && x1_lds_bytes(qtype, job.k) <= 64 * 1024) {
       if (qtype == kQ4_K) return launch_x1<kQ4_K, false, MODE, 2, 1, false, true>(job, s);

@@ -55,6 +55,11 @@ def test_gemv_bias_and_q6k_upstream_layout():
     check_close(y, ref, "bias")
     y, ref = _run(Q6_K | 0x100, 300, 2048, 2, torch.bfloat16, seed=6)
     check_close(y, ref, "q6k d-last")
+    # the matrix-core path (16-row tiles, 8..16 activation rows) in both field orders
+    for qt in (Q6_K, Q6_K | 0x100):
+        for m in (8, 13, 16):
+            y, ref = _run(qt, 512, 2048, m, torch.bfloat16, seed=7 + m)
+            check_close(y, ref, f"q6k {qt} mfma m={m}")
 
 
 def test_linear_dispatch_large_m_float32():

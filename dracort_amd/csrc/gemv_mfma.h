@@ -21,6 +21,8 @@
 // kSwiGLU (gate and up tiles side by side), kResid.
 #pragma once
 
+#include <climits>
+
 #include "gemv_stream.h"
 
 namespace draco {
@@ -181,6 +183,42 @@ __device__ __forceinline__ void mf_load_x(const void* __restrict__ xrow, int p, 
   }
 }
 
+// acc += the products of one 256-element chunk: activations x (per group, NP
+// bf16 planes) against NR weight rows' codes w.
+template <int QT, bool XBF16, int NR>
+__device__ __forceinline__ void mf_chunk_q4(const mf_bf16x8 (&x)[8][XBF16 ? 1 : 3], const MfChunk<QT> (&w)[NR],
+                                            int q, mf_f32x4 (&acc)[NR]) {
+  constexpr int NP = XBF16 ? 1 : 3;
+  const uint32_t ones[4] = {kOnePair, kOnePair, kOnePair, kOnePair};
+  const mf_bf16x8 bones = __builtin_bit_cast(mf_bf16x8, ones);
+  float a[NR][8], cb[NR][8];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) mf_coeffs<QT>(w[r], a[r], cb[r]);
+  const mf_f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    mf_f32x4 sg = z;
+#pragma unroll
+    for (int j = NP - 1; j >= 0; --j) sg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[g][j], bones, sg, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const mf_bf16x8 bc = XBF16 ? mf_codes<QT>(w[r], g, q) : mf_codes_exact<QT>(w[r], g, q);
+      mf_f32x4 dg = z;
+#pragma unroll
+      for (int j = NP - 1; j >= 0; --j) dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[g][j], bc, dg, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        // sum x * (code - off) = D - (bias + off) S, formed with one rounding
+        // before it is scaled (the bias must cancel here, not in the running sum)
+        const float bias = (XBF16 ? kCodeBias : 0.f) + MfOff<QT>::value;
+        const float xcode = fmaf(-bias, sg[v], dg[v]);
+        if constexpr (QT == kQ4_K) acc[r][v] = fmaf(cb[r][g], sg[v], acc[r][v]);
+        acc[r][v] = fmaf(a[r][g], xcode, acc[r][v]);
+      }
+    }
+  }
+}
+
 // acc (the lane's 4 values of the 16 x 16 tile) += the products over the
 // 256-element chunks ks, ks + 4, ... < chunks of NR weight rows (buffer
 // resources rs, the lane's row at byte offset rowoff) with the lane's
@@ -190,8 +228,6 @@ template <int QT, bool XBF16, int NR>
 __device__ __forceinline__ void mf_accumulate(const __amdgpu_buffer_rsrc_t (&rs)[NR], int rowoff,
                                               const void* __restrict__ xrow, int q, int ks, int chunks,
                                               mf_f32x4 (&acc)[NR]) {
-  const uint32_t ones[4] = {kOnePair, kOnePair, kOnePair, kOnePair};
-  const mf_bf16x8 bones = __builtin_bit_cast(mf_bf16x8, ones);
   // two buffer sets used alternately (no copies)
   constexpr int NP = XBF16 ? 1 : 3;
   MfChunk<QT> wb[2][NR];
@@ -202,41 +238,7 @@ __device__ __forceinline__ void mf_accumulate(const __amdgpu_buffer_rsrc_t (&rs)
 #pragma unroll
     for (int r = 0; r < NR; ++r) wb[slot][r] = mf_load<QT>(rs[r], rowoff, cc, q);
   };
-  auto compute_chunk = [&](int slot) {
-    float a[NR][8], cb[NR][8];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) mf_coeffs<QT>(wb[slot][r], a[r], cb[r]);
-    const mf_f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    mf_f32x4 sg[8], dg[NR][8];
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-      sg[g] = z;
-#pragma unroll
-      for (int j = NP - 1; j >= 0; --j)
-        sg[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[slot][g][j], bones, sg[g], 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const mf_bf16x8 bc = XBF16 ? mf_codes<QT>(wb[slot][r], g, q) : mf_codes_exact<QT>(wb[slot][r], g, q);
-        dg[r][g] = z;
-#pragma unroll
-        for (int j = NP - 1; j >= 0; --j)
-          dg[r][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb[slot][g][j], bc, dg[r][g], 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < 8; ++g)
-#pragma unroll
-      for (int r = 0; r < NR; ++r)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          // sum x * (code - off) = D - (bias + off) S, formed with one rounding
-          // before it is scaled (the bias must cancel here, not in the running sum)
-          const float bias = (XBF16 ? kCodeBias : 0.f) + MfOff<QT>::value;
-          const float xcode = fmaf(-bias, sg[g][v], dg[r][g][v]);
-          if constexpr (QT == kQ4_K) acc[r][v] = fmaf(cb[r][g], sg[g][v], acc[r][v]);
-          acc[r][v] = fmaf(a[r][g], xcode, acc[r][v]);
-        }
-  };
+  auto compute_chunk = [&](int slot) { mf_chunk_q4<QT, XBF16, NR>(xb[slot], wb[slot], q, acc); };
   if (ks < chunks) load_chunk(0, ks);
   for (int c = ks; c < chunks; c += 8) {
     if (c + 4 < chunks) load_chunk(1, c + 4);
@@ -300,12 +302,36 @@ __device__ __forceinline__ mf_s16x4 mf_codes_q6(const MfQ6& c, int g) {
   return __builtin_bit_cast(mf_s16x4, v);
 }
 
+template <int NR>
+__device__ __forceinline__ void mf_chunk_q6(const uint2 (&x)[16], const MfQ6 (&w)[NR], mf_f32x4 (&acc)[NR]) {
+  const uint32_t ones2[2] = {kOnePair, kOnePair};
+  const mf_s16x4 bones = __builtin_bit_cast(mf_s16x4, ones2);
+  float a[NR][16];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const float d = f16_bits_to_f32(w[r].d);
+    const uint32_t sw[4] = {w[r].sc.x, w[r].sc.y, w[r].sc.z, w[r].sc.w};
+#pragma unroll
+    for (int g = 0; g < 16; ++g) a[r][g] = d * sbyte_f(sw[g >> 2], g & 3);
+  }
+  const mf_f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int g = 0; g < 16; ++g) {
+    const mf_s16x4 av = __builtin_bit_cast(mf_s16x4, x[g]);
+    const mf_f32x4 sg = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bones, z, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const mf_f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, mf_codes_q6(w[r], g), z, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[r][v] = fmaf(a[r][g], fmaf(-(kCodeBias + 32.f), sg[v], dg[v]), acc[r][v]);
+    }
+  }
+}
+
 template <bool DL, int NR>
 __device__ __forceinline__ void mf_accumulate_q6k(const __amdgpu_buffer_rsrc_t (&rs)[NR], int rowoff,
                                                   const void* __restrict__ xrow, int q, int ks, int chunks,
                                                   mf_f32x4 (&acc)[NR]) {
-  const uint32_t ones2[2] = {kOnePair, kOnePair};
-  const mf_s16x4 bones = __builtin_bit_cast(mf_s16x4, ones2);
   const uint16_t* x = static_cast<const uint16_t*>(xrow);
   MfQ6 wb[2][NR];
   uint2 xb[2][16];
@@ -315,28 +341,7 @@ __device__ __forceinline__ void mf_accumulate_q6k(const __amdgpu_buffer_rsrc_t (
 #pragma unroll
     for (int r = 0; r < NR; ++r) wb[slot][r] = mf_load_q6<DL>(rs[r], rowoff, cc, q);
   };
-  auto compute_chunk = [&](int slot) {
-    float a[NR][16];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const float d = f16_bits_to_f32(wb[slot][r].d);
-      const uint32_t sw[4] = {wb[slot][r].sc.x, wb[slot][r].sc.y, wb[slot][r].sc.z, wb[slot][r].sc.w};
-#pragma unroll
-      for (int g = 0; g < 16; ++g) a[r][g] = d * sbyte_f(sw[g >> 2], g & 3);
-    }
-    const mf_f32x4 z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      const mf_s16x4 av = __builtin_bit_cast(mf_s16x4, xb[slot][g]);
-      const mf_f32x4 sg = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bones, z, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const mf_f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, mf_codes_q6(wb[slot][r], g), z, 0, 0, 0);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[r][v] = fmaf(a[r][g], fmaf(-(kCodeBias + 32.f), sg[v], dg[v]), acc[r][v]);
-      }
-    }
-  };
+  auto compute_chunk = [&](int slot) { mf_chunk_q6<NR>(xb[slot], wb[slot], acc); };
   if (ks < chunks) load_chunk(0, ks);
   for (int c = ks; c < chunks; c += 8) {
     if (c + 4 < chunks) load_chunk(1, c + 4);
@@ -424,6 +429,173 @@ __global__ __launch_bounds__(TPW * 256) void gemv_mfma_kernel(StreamJob job) {
   }
 }
 
+// Persistent form for bf16 activations and K <= 4096 (at most 16 chunks): a
+// fixed grid of workgroups walks the 16-row weight tiles (tile t, t + grid,
+// ...).  Wave ks of a workgroup always takes chunks ks, ks + 4, ks + 8,
+// ks + 12, so its activation fragments are loaded into registers once for
+// the whole launch; per tile it streams only the weights, with the next
+// tile's weights requested before the current tile's math (an empty buffer
+// resource past the last tile or chunk keeps every wait count exact).  The
+// four partial tiles meet in LDS (double-buffered, one barrier per tile) and
+// wave 0 stores the result while the others go on.
+template <int QT> struct MfpTypes;
+template <> struct MfpTypes<kQ4_K> { typedef MfChunk<kQ4_K> W; typedef mf_bf16x8 X[8][1]; };
+template <> struct MfpTypes<kQ4_0> { typedef MfChunk<kQ4_0> W; typedef mf_bf16x8 X[8][1]; };
+template <> struct MfpTypes<kQ6_K> { typedef MfQ6 W; typedef uint2 X[16]; };
+
+template <int QT, bool DL, int MODE, int W>
+__global__ __launch_bounds__(W * 64) void gemv_mfp_kernel(StreamJob job) {
+  constexpr int NR = MODE == kSwiGLU ? 2 : 1;
+  constexpr int CPW = 16 / W;  // chunks per wave (W waves split the at most 16 chunks)
+  typedef typename MfpTypes<QT>::W WChunk;
+  __shared__ mf_f32x4 part[2][W][NR][64];
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, nl = lane & 15;
+  const int k = job.k, M = job.m;
+  const int chunks = k >> 8;
+  const int ntiles = job.rows >> 4;
+  const int my_tiles = ntiles > (int)blockIdx.x ? (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+
+  // the wave's activations, resident for the launch (rows past M repeat row M - 1)
+  typename MfpTypes<QT>::X xr[CPW];
+  {
+    const uint16_t* xrow = static_cast<const uint16_t*>(job.x) + (size_t)min(nl, M - 1) * k;
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const int cc = min(ks + W * j, chunks - 1);
+      if constexpr (QT == kQ6_K) {
+#pragma unroll
+        for (int g = 0; g < 16; ++g) xr[j][g] = *reinterpret_cast<const uint2*>(xrow + cc * 256 + 16 * g + 4 * q);
+      } else {
+#pragma unroll
+        for (int g = 0; g < 8; ++g) mf_load_x<true>(xrow, cc * 256 + mf_pos<QT>(g, q), xr[j][g]);
+      }
+    }
+  }
+
+  // matrices of the launch (kPlain: row tiles of up to four matrices back to back)
+  int c1 = INT_MAX, c2 = INT_MAX, c3 = INT_MAX;
+  if constexpr (MODE == kPlain) {
+    if (job.n_mats > 1) c1 = job.n[0];
+    if (job.n_mats > 2) c2 = c1 + job.n[1];
+    if (job.n_mats > 3) c3 = c2 + job.n[2];
+  }
+  const __amdgpu_buffer_rsrc_t empty = make_rsrc(job.w[0], 0u);
+
+  auto load_tile = [&](int i, WChunk (&dst)[CPW][NR]) {
+    const int t = (int)blockIdx.x + i * (int)gridDim.x;
+    const bool live = i < my_tiles;
+    const int row = live ? 16 * t : 0;
+    int mat = 0, base = 0;
+    if constexpr (MODE == kPlain) {
+      mat = (row >= c1) + (row >= c2) + (row >= c3);
+      base = mat == 0 ? 0 : mat == 1 ? c1 : mat == 2 ? c2 : c3;
+    }
+    const int rowoff = (row - base + nl) * job.row_bytes;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      // the matrix's base and size picked as scalars, its resource built here
+      // (an array of resources indexed by a runtime value goes to scratch)
+      const int mm = NR == 2 ? r : mat;
+      const uint8_t* wp = mm == 0 ? job.w[0] : mm == 1 ? job.w[1] : mm == 2 ? job.w[2] : job.w[3];
+      const int nn = mm == 0 ? job.n[0] : mm == 1 ? job.n[1] : mm == 2 ? job.n[2] : job.n[3];
+      const __amdgpu_buffer_rsrc_t rs = live ? make_rsrc(wp, (uint32_t)((int64_t)nn * job.row_bytes)) : empty;
+#pragma unroll
+      for (int j = 0; j < CPW; ++j) {
+        const int cc = ks + W * j;
+        const __amdgpu_buffer_rsrc_t rj = cc < chunks ? rs : empty;
+        if constexpr (QT == kQ6_K)
+          dst[j][r] = mf_load_q6<DL>(rj, rowoff, min(cc, chunks - 1), q);
+        else
+          dst[j][r] = mf_load<QT>(rj, rowoff, min(cc, chunks - 1), q);
+      }
+    }
+  };
+
+  WChunk wb[2][CPW][NR];
+  load_tile(0, wb[0]);
+  for (int i0 = 0; i0 < my_tiles; i0 += 2) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int i = i0 + p;
+      load_tile(i + 1, wb[p ^ 1]);
+      __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the math
+      if (i < my_tiles) {
+        mf_f32x4 acc[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) acc[r] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < CPW; ++j) {
+          if (ks + W * j < chunks) {
+            if constexpr (QT == kQ6_K)
+              mf_chunk_q6<NR>(xr[j], wb[p][j], acc);
+            else
+              mf_chunk_q4<QT, true, NR>(xr[j], wb[p][j], q, acc);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < NR; ++r) part[p][ks][r][lane] = acc[r];
+      }
+      __syncthreads();
+      if (i < my_tiles && ks == 0) {
+        mf_f32x4 tot[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          tot[r] = part[p][0][r][lane];
+#pragma unroll
+          for (int j = 1; j < W; ++j) {
+            const mf_f32x4 pp = part[p][j][r][lane];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) tot[r][v] += pp[v];
+          }
+        }
+        const int orow = 16 * ((int)blockIdx.x + i * (int)gridDim.x) + nl;
+        int omat = 0, olrow = orow;
+        if constexpr (MODE == kPlain) {
+          omat = (orow >= c1) + (orow >= c2) + (orow >= c3);
+          olrow = orow - (omat == 0 ? 0 : omat == 1 ? c1 : omat == 2 ? c2 : c3);
+        }
+        const int n = MODE == kPlain ? (omat == 0 ? job.n[0] : omat == 1 ? job.n[1] : omat == 2 ? job.n[2] : job.n[3])
+                                     : job.n[0];
+        float* yp = job.y[0];
+        uint16_t* ybp = job.yb[0];
+        if constexpr (MODE == kPlain) {
+          yp = omat == 0 ? job.y[0] : omat == 1 ? job.y[1] : omat == 2 ? job.y[2] : job.y[3];
+          ybp = omat == 0 ? job.yb[0] : omat == 1 ? job.yb[1] : omat == 2 ? job.yb[2] : job.yb[3];
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = 4 * q + v;
+          if (m >= M) continue;
+          const size_t o = (size_t)m * n + olrow;
+          if constexpr (MODE == kResid) {
+            const float out = job.resid[o] + tot[0][v];
+            job.resid[o] = out;
+            if (job.resid_bf16) job.resid_bf16[o] = f32_to_bf16_rne(out);
+          } else {
+            float out = tot[0][v];
+            if constexpr (MODE == kSwiGLU) out = silu(tot[0][v]) * tot[1][v];
+            if (MODE == kPlain && job.bias) out += job.bias[olrow];
+            if (yp) yp[o] = out;
+            if (ybp) ybp[o] = f32_to_bf16_rne(out);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int QT, bool DL, int MODE, int W>
+static int launch_gemv_mfp(const StreamJob& job, int blocks_per_cu, hipStream_t s) {
+  if (job.k > 4096 || job.k % 256 != 0 || job.rows % 16 != 0)
+    return set_error(DRACO_EINVAL_SHAPE, "persistent matrix-core GEMV takes K <= 4096 and whole 16-row tiles");
+  const int tiles = job.rows / 16;
+  const int blocks = std::max(1, std::min(tiles, device_cus() * blocks_per_cu));
+  hipLaunchKernelGGL((gemv_mfp_kernel<QT, DL, MODE, W>), dim3(blocks), dim3(W * 64), 0, s, job);
+  return check_launch("gemv_mfp");
+}
+
 // Whether the matrix-core GEMV takes this launch: K-quant Q4_K or Q4_0,
 // 2..16 activation rows, K a multiple of 256, every matrix a whole number of
 // 16-row tiles, 32-bit buffer offsets.
@@ -443,16 +615,31 @@ static int launch_gemv_mfma(const StreamJob& job, hipStream_t s) {
   const int tiles = (job.rows + 15) / 16;
   // two tiles per workgroup for very tall matrices (bf16 only: with float32
   // activations the 512-thread form would spill registers)
-  if (XBF16 && tiles >= 2048) {
-    hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 2>), dim3((tiles + 1) / 2), dim3(512), 0, s, job);
-  } else {
-    hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 1>), dim3(tiles), dim3(256), 0, s, job);
+  if constexpr (XBF16) {
+    if (tiles >= 2048) {
+      hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 2>), dim3((tiles + 1) / 2), dim3(512), 0, s, job);
+      return check_launch("gemv_mfma");
+    }
   }
+  hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 1>), dim3(tiles), dim3(256), 0, s, job);
   return check_launch("gemv_mfma");
 }
 
 template <int MODE>
 static int gemv_mfma_dispatch(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s) {
+  // bf16 rows of at most 16 chunks: the persistent form (activations resident
+  // in registers), one 512-thread workgroup per CU (measured best: 14336 x 4096
+  // Q4_K at M = 16 18 us vs 30 us for the one-tile-per-workgroup form)
+  // (SwiGLU's two weight sets fit the 512-thread register budget for Q4_K only)
+  if (xbf16 && job.k <= 4096 && (MODE != kSwiGLU || qtype == kQ4_K)) {
+    if constexpr (MODE != kSwiGLU) {
+      if (qtype == kQ6_K)
+        return d_last ? launch_gemv_mfp<kQ6_K, true, MODE, 8>(job, 1, s)
+                      : launch_gemv_mfp<kQ6_K, false, MODE, 8>(job, 1, s);
+    }
+    if (qtype == kQ4_K) return launch_gemv_mfp<kQ4_K, false, MODE, 8>(job, 1, s);
+    if constexpr (MODE != kSwiGLU) return launch_gemv_mfp<kQ4_0, false, MODE, 8>(job, 1, s);
+  }
   if (qtype == kQ6_K)
     return d_last ? launch_gemv_mfma<kQ6_K, true, true, MODE>(job, s) : launch_gemv_mfma<kQ6_K, false, true, MODE>(job, s);
   if (qtype == kQ4_K)

@@ -265,6 +265,51 @@ def traffic_probe(reps: int):
     log(f"traffic probe: {reps} copies of {src.numel()} bytes")
 
 
+def mfma_probe(reps: int):
+    """The prefill GEMMs of configuration 4, launched eagerly ``reps`` times
+    each, for the matrix-core counter runs."""
+    import torch
+
+    from dracort_amd.kernels import gemm_workspace_bytes, gguf_gemm
+    from dracort_amd.runtime.decode import synthetic_weight
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    for n, k in ((14336, 4096), (4096, 14336)):
+        w = synthetic_weight(n, k, 12, gen, "cuda")
+        for m in (512, 2048):
+            x = torch.randn((m, k), device="cuda").to(torch.bfloat16)
+            y = torch.empty((m, n), device="cuda")
+            ws = torch.empty(gemm_workspace_bytes(12, m, k), dtype=torch.uint8, device="cuda")
+            for _ in range(reps):
+                gguf_gemm(x, w.data, 12, (n, k), out=y, workspace=ws)
+            torch.cuda.synchronize()
+            log(f"mfma probe: [{n},{k}] m={m} x{reps}")
+
+
+def moe_probe(reps: int):
+    """Configuration 5's MoE FFN launched eagerly ``reps`` times (kernel traces)."""
+    import torch
+
+    from dracort_amd.kernels import gguf_moe, moe_workspace_bytes
+    from dracort_amd.runtime.decode import synthetic_weight
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    hid, inter, ne, tok = 4096, 14336, 8, 64
+    wg = [synthetic_weight(inter, hid, 12, gen, "cuda").data for _ in range(ne)]
+    wu = [synthetic_weight(inter, hid, 12, gen, "cuda").data for _ in range(ne)]
+    wd = [synthetic_weight(hid, inter, 12, gen, "cuda").data for _ in range(ne)]
+    x = torch.randn((tok, hid), device="cuda").to(torch.bfloat16)
+    logits = torch.randn((tok, ne), device="cuda")
+    ws = torch.empty(moe_workspace_bytes(tok, hid, inter, ne, 2), dtype=torch.uint8, device="cuda")
+    y = torch.empty((tok, hid), device="cuda")
+    for _ in range(reps):
+        gguf_moe(x, logits, wg, wu, wd, 12, inter, top_k=2, workspace=ws, out=y)
+    torch.cuda.synchronize()
+    log(f"moe probe: x{reps}")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -277,6 +322,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--suite", action="store_true", help="measure configurations 1, 2, 4, 5 (one JSON line each)")
     ap.add_argument("--traffic-probe", action="store_true", help="run only the roofline rotation + a 256 MB copy")
+    ap.add_argument("--mfma-probe", action="store_true", help="run only the configuration-4 GEMMs (counter runs)")
+    ap.add_argument("--moe-probe", action="store_true", help="run only the configuration-5 MoE FFN (kernel traces)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -301,6 +348,12 @@ def main() -> int:
         return 0
     if args.traffic_probe:
         traffic_probe(args.roofline_reps)
+        return 0
+    if args.mfma_probe:
+        mfma_probe(3)
+        return 0
+    if args.moe_probe:
+        moe_probe(3)
         return 0
     shape = LlamaShape()
     t0 = time.time()

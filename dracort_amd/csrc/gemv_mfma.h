@@ -219,22 +219,49 @@ __device__ __forceinline__ void mf_chunk_q4(const mf_bf16x8 (&x)[8][XBF16 ? 1 : 
   }
 }
 
+// The three bf16 planes of a float32 value (hi, mid, lo: each the
+// round-to-nearest bf16 of what the previous ones leave; the split
+// mf_load_x does on the fly).
+__device__ __forceinline__ void mf_split3(float v, uint16_t& hi, uint16_t& mid, uint16_t& lo) {
+  const uint32_t a = f32_to_bf16_rne(v);
+  const float r1 = v - __uint_as_float(a << 16);
+  const uint32_t b = f32_to_bf16_rne(r1);
+  hi = (uint16_t)a;
+  mid = (uint16_t)b;
+  lo = (uint16_t)f32_to_bf16_rne(r1 - __uint_as_float(b << 16));
+}
+
 // acc (the lane's 4 values of the 16 x 16 tile) += the products over the
 // 256-element chunks ks, ks + 4, ... < chunks of NR weight rows (buffer
 // resources rs, the lane's row at byte offset rowoff) with the lane's
 // activation row xrow.  Software pipeline: the activations and codes of chunk
 // c + 4 are loaded while chunk c is multiplied.
-template <int QT, bool XBF16, int NR>
+//
+// XPL: the activations are already three bf16 planes (hi, mid, lo of a float32
+// row, as mf_split3 writes them) at xrow, xrow + pstride, xrow + 2 pstride
+// (uint16 elements); no split on the fly.
+template <int QT, bool XBF16, int NR, bool XPL = false>
 __device__ __forceinline__ void mf_accumulate(const __amdgpu_buffer_rsrc_t (&rs)[NR], int rowoff,
                                               const void* __restrict__ xrow, int q, int ks, int chunks,
-                                              mf_f32x4 (&acc)[NR]) {
+                                              mf_f32x4 (&acc)[NR], size_t pstride = 0) {
+  static_assert(!(XPL && XBF16), "pre-split planes carry float32 activations");
   // two buffer sets used alternately (no copies)
   constexpr int NP = XBF16 ? 1 : 3;
   MfChunk<QT> wb[2][NR];
   mf_bf16x8 xb[2][8][NP];
   auto load_chunk = [&](int slot, int cc) {
 #pragma unroll
-    for (int g = 0; g < 8; ++g) mf_load_x<XBF16>(xrow, cc * 256 + mf_pos<QT>(g, q), xb[slot][g]);
+    for (int g = 0; g < 8; ++g) {
+      const int p = cc * 256 + mf_pos<QT>(g, q);
+      if constexpr (XPL) {
+        const uint16_t* xp = static_cast<const uint16_t*>(xrow) + p;
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+          xb[slot][g][j] = __builtin_bit_cast(mf_bf16x8, *reinterpret_cast<const uint4*>(xp + j * pstride));
+      } else {
+        mf_load_x<XBF16>(xrow, p, xb[slot][g]);
+      }
+    }
 #pragma unroll
     for (int r = 0; r < NR; ++r) wb[slot][r] = mf_load<QT>(rs[r], rowoff, cc, q);
   };
@@ -443,64 +470,50 @@ template <> struct MfpTypes<kQ4_K> { typedef MfChunk<kQ4_K> W; typedef mf_bf16x8
 template <> struct MfpTypes<kQ4_0> { typedef MfChunk<kQ4_0> W; typedef mf_bf16x8 X[8][1]; };
 template <> struct MfpTypes<kQ6_K> { typedef MfQ6 W; typedef uint2 X[16]; };
 
-template <int QT, bool DL, int MODE, int W>
-__global__ __launch_bounds__(W * 64) void gemv_mfp_kernel(StreamJob job) {
-  constexpr int NR = MODE == kSwiGLU ? 2 : 1;
-  constexpr int CPW = 16 / W;  // chunks per wave (W waves split the at most 16 chunks)
+// The wave's activation fragments (chunks ks, ks + W, ... of token row xrow).
+template <int QT, int W>
+__device__ __forceinline__ void mfp_load_x(const uint16_t* __restrict__ xrow, int chunks, int ks, int q,
+                                           typename MfpTypes<QT>::X (&xr)[16 / W]) {
+#pragma unroll
+  for (int j = 0; j < 16 / W; ++j) {
+    const int cc = min(ks + W * j, chunks - 1);
+    if constexpr (QT == kQ6_K) {
+#pragma unroll
+      for (int g = 0; g < 16; ++g) xr[j][g] = *reinterpret_cast<const uint2*>(xrow + cc * 256 + 16 * g + 4 * q);
+    } else {
+#pragma unroll
+      for (int g = 0; g < 8; ++g) mf_load_x<true>(xrow, cc * 256 + mf_pos<QT>(g, q), xr[j][g]);
+    }
+  }
+}
+
+// A weight row as seen by one lane: its matrix's buffer resource and the row's
+// byte offset.
+struct MfRow {
+  __amdgpu_buffer_rsrc_t rs;
+  int rowoff;
+};
+
+// Streams this workgroup's ntiles weight tiles against resident activations.
+// tile_rsrc(i, r) gives matrix r's resource and the lane's row offset for
+// tile i (an MfRow; called for i < ntiles only); emit(i, tot) runs on wave 0 with tile
+// i's summed 16 x 16 result.  Ends in a barrier (the partial buffers are free).
+template <int QT, bool DL, int NR, int W, class TileRsrc, class Emit>
+__device__ __forceinline__ void mfp_stream(const typename MfpTypes<QT>::X (&xr)[16 / W], int chunks, int ntiles,
+                                           __amdgpu_buffer_rsrc_t empty, TileRsrc tile_rsrc, Emit emit,
+                                           mf_f32x4 (&part)[2][W][NR][64]) {
+  constexpr int CPW = 16 / W;
   typedef typename MfpTypes<QT>::W WChunk;
-  __shared__ mf_f32x4 part[2][W][NR][64];
   const int lane = threadIdx.x & 63;
   const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int q = lane >> 4, nl = lane & 15;
-  const int k = job.k, M = job.m;
-  const int chunks = k >> 8;
-  const int ntiles = job.rows >> 4;
-  const int my_tiles = ntiles > (int)blockIdx.x ? (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
-
-  // the wave's activations, resident for the launch (rows past M repeat row M - 1)
-  typename MfpTypes<QT>::X xr[CPW];
-  {
-    const uint16_t* xrow = static_cast<const uint16_t*>(job.x) + (size_t)min(nl, M - 1) * k;
-#pragma unroll
-    for (int j = 0; j < CPW; ++j) {
-      const int cc = min(ks + W * j, chunks - 1);
-      if constexpr (QT == kQ6_K) {
-#pragma unroll
-        for (int g = 0; g < 16; ++g) xr[j][g] = *reinterpret_cast<const uint2*>(xrow + cc * 256 + 16 * g + 4 * q);
-      } else {
-#pragma unroll
-        for (int g = 0; g < 8; ++g) mf_load_x<true>(xrow, cc * 256 + mf_pos<QT>(g, q), xr[j][g]);
-      }
-    }
-  }
-
-  // matrices of the launch (kPlain: row tiles of up to four matrices back to back)
-  int c1 = INT_MAX, c2 = INT_MAX, c3 = INT_MAX;
-  if constexpr (MODE == kPlain) {
-    if (job.n_mats > 1) c1 = job.n[0];
-    if (job.n_mats > 2) c2 = c1 + job.n[1];
-    if (job.n_mats > 3) c3 = c2 + job.n[2];
-  }
-  const __amdgpu_buffer_rsrc_t empty = make_rsrc(job.w[0], 0u);
-
+  const int q = lane >> 4;
   auto load_tile = [&](int i, WChunk (&dst)[CPW][NR]) {
-    const int t = (int)blockIdx.x + i * (int)gridDim.x;
-    const bool live = i < my_tiles;
-    const int row = live ? 16 * t : 0;
-    int mat = 0, base = 0;
-    if constexpr (MODE == kPlain) {
-      mat = (row >= c1) + (row >= c2) + (row >= c3);
-      base = mat == 0 ? 0 : mat == 1 ? c1 : mat == 2 ? c2 : c3;
-    }
-    const int rowoff = (row - base + nl) * job.row_bytes;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      // the matrix's base and size picked as scalars, its resource built here
-      // (an array of resources indexed by a runtime value goes to scratch)
-      const int mm = NR == 2 ? r : mat;
-      const uint8_t* wp = mm == 0 ? job.w[0] : mm == 1 ? job.w[1] : mm == 2 ? job.w[2] : job.w[3];
-      const int nn = mm == 0 ? job.n[0] : mm == 1 ? job.n[1] : mm == 2 ? job.n[2] : job.n[3];
-      const __amdgpu_buffer_rsrc_t rs = live ? make_rsrc(wp, (uint32_t)((int64_t)nn * job.row_bytes)) : empty;
+      MfRow row{empty, 0};
+      if (i < ntiles) row = tile_rsrc(i, r);
+      const __amdgpu_buffer_rsrc_t rs = row.rs;
+      const int rowoff = row.rowoff;
 #pragma unroll
       for (int j = 0; j < CPW; ++j) {
         const int cc = ks + W * j;
@@ -512,16 +525,15 @@ __global__ __launch_bounds__(W * 64) void gemv_mfp_kernel(StreamJob job) {
       }
     }
   };
-
   WChunk wb[2][CPW][NR];
   load_tile(0, wb[0]);
-  for (int i0 = 0; i0 < my_tiles; i0 += 2) {
+  for (int i0 = 0; i0 < ntiles; i0 += 2) {
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       const int i = i0 + p;
       load_tile(i + 1, wb[p ^ 1]);
       __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the math
-      if (i < my_tiles) {
+      if (i < ntiles) {
         mf_f32x4 acc[NR];
 #pragma unroll
         for (int r = 0; r < NR; ++r) acc[r] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
@@ -538,7 +550,7 @@ __global__ __launch_bounds__(W * 64) void gemv_mfp_kernel(StreamJob job) {
         for (int r = 0; r < NR; ++r) part[p][ks][r][lane] = acc[r];
       }
       __syncthreads();
-      if (i < my_tiles && ks == 0) {
+      if (i < ntiles && ks == 0) {
         mf_f32x4 tot[NR];
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
@@ -550,40 +562,99 @@ __global__ __launch_bounds__(W * 64) void gemv_mfp_kernel(StreamJob job) {
             for (int v = 0; v < 4; ++v) tot[r][v] += pp[v];
           }
         }
-        const int orow = 16 * ((int)blockIdx.x + i * (int)gridDim.x) + nl;
-        int omat = 0, olrow = orow;
-        if constexpr (MODE == kPlain) {
-          omat = (orow >= c1) + (orow >= c2) + (orow >= c3);
-          olrow = orow - (omat == 0 ? 0 : omat == 1 ? c1 : omat == 2 ? c2 : c3);
-        }
-        const int n = MODE == kPlain ? (omat == 0 ? job.n[0] : omat == 1 ? job.n[1] : omat == 2 ? job.n[2] : job.n[3])
-                                     : job.n[0];
-        float* yp = job.y[0];
-        uint16_t* ybp = job.yb[0];
-        if constexpr (MODE == kPlain) {
-          yp = omat == 0 ? job.y[0] : omat == 1 ? job.y[1] : omat == 2 ? job.y[2] : job.y[3];
-          ybp = omat == 0 ? job.yb[0] : omat == 1 ? job.yb[1] : omat == 2 ? job.yb[2] : job.yb[3];
-        }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int m = 4 * q + v;
-          if (m >= M) continue;
-          const size_t o = (size_t)m * n + olrow;
-          if constexpr (MODE == kResid) {
-            const float out = job.resid[o] + tot[0][v];
-            job.resid[o] = out;
-            if (job.resid_bf16) job.resid_bf16[o] = f32_to_bf16_rne(out);
-          } else {
-            float out = tot[0][v];
-            if constexpr (MODE == kSwiGLU) out = silu(tot[0][v]) * tot[1][v];
-            if (MODE == kPlain && job.bias) out += job.bias[olrow];
-            if (yp) yp[o] = out;
-            if (ybp) ybp[o] = f32_to_bf16_rne(out);
-          }
-        }
+        emit(i, tot);
       }
     }
   }
+  __syncthreads();
+}
+
+template <int QT, bool DL, int MODE, int W>
+__global__ __launch_bounds__(W * 64) void gemv_mfp_kernel(StreamJob job) {
+  constexpr int NR = MODE == kSwiGLU ? 2 : 1;
+  __shared__ mf_f32x4 part[2][W][NR][64];
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, nl = lane & 15;
+  const int k = job.k, M = job.m;
+  const int chunks = k >> 8;
+  const int ntiles = job.rows >> 4;
+  const int my_tiles = ntiles > (int)blockIdx.x ? (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+
+  // the wave's activations, resident for the launch (rows past M repeat row M - 1)
+  typename MfpTypes<QT>::X xr[16 / W];
+  mfp_load_x<QT, W>(static_cast<const uint16_t*>(job.x) + (size_t)min(nl, M - 1) * k, chunks, ks, q, xr);
+
+  // matrices of the launch (kPlain: row tiles of up to four matrices back to back)
+  int c1 = INT_MAX, c2 = INT_MAX, c3 = INT_MAX;
+  if constexpr (MODE == kPlain) {
+    if (job.n_mats > 1) c1 = job.n[0];
+    if (job.n_mats > 2) c2 = c1 + job.n[1];
+    if (job.n_mats > 3) c3 = c2 + job.n[2];
+  }
+  // the launch's pointers and sizes as scalars (the lambdas below copy them;
+  // a copy of the whole argument would be indexed at run time, from scratch)
+  const uint8_t *w0 = job.w[0], *w1 = job.w[1], *w2 = job.w[2], *w3 = job.w[3];
+  const int n0 = job.n[0], n1 = job.n[1], n2 = job.n[2], n3 = job.n[3];
+  float *y0 = job.y[0], *y1 = job.y[1], *y2 = job.y[2], *y3 = job.y[3];
+  uint16_t *b0 = job.yb[0], *b1 = job.yb[1], *b2 = job.yb[2], *b3 = job.yb[3];
+  float* const resid = job.resid;
+  uint16_t* const resid_bf16 = job.resid_bf16;
+  const float* const bias = job.bias;
+  const int row_bytes = job.row_bytes;
+  // (chains of selects on a running value: a select keyed by an index would be
+  // turned into a table lookup in scratch)
+  auto pick = [](int mat, auto v0, auto v1, auto v2, auto v3) {
+    auto v = v0;
+    v = mat >= 1 ? v1 : v;
+    v = mat >= 2 ? v2 : v;
+    v = mat >= 3 ? v3 : v;
+    return v;
+  };
+  auto locate = [=](int row, int& mat, int& lrow) {
+    mat = 0;
+    lrow = row;
+    if constexpr (MODE == kPlain) {
+      mat = (row >= c1) + (row >= c2) + (row >= c3);
+      int base = row >= c1 ? c1 : 0;
+      base = row >= c2 ? c2 : base;
+      base = row >= c3 ? c3 : base;
+      lrow = row - base;
+    }
+  };
+  auto tile_rsrc = [=](int i, int r) {
+    int mat, lrow;
+    locate(16 * ((int)blockIdx.x + i * (int)gridDim.x), mat, lrow);
+    const int mm = NR == 2 ? r : mat;
+    const uint8_t* wp = pick(mm, w0, w1, w2, w3);
+    const int nn = pick(mm, n0, n1, n2, n3);
+    return MfRow{make_rsrc(wp, (uint32_t)((int64_t)nn * row_bytes)), (lrow + nl) * row_bytes};
+  };
+  auto emit = [=](int i, const mf_f32x4 (&tot)[NR]) {
+    int omat, olrow;
+    locate(16 * ((int)blockIdx.x + i * (int)gridDim.x) + nl, omat, olrow);
+    const int n = pick(omat, n0, n1, n2, n3);
+    float* const yp = pick(omat, y0, y1, y2, y3);
+    uint16_t* const ybp = pick(omat, b0, b1, b2, b3);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 4 * q + v;  // D layout: lane l holds rows 4 (l / 16) + v, column l % 16
+      if (m >= M) continue;
+      const size_t o = (size_t)m * n + olrow;
+      if constexpr (MODE == kResid) {
+        const float out = resid[o] + tot[0][v];
+        resid[o] = out;
+        if (resid_bf16) resid_bf16[o] = f32_to_bf16_rne(out);
+      } else {
+        float out = tot[0][v];
+        if constexpr (MODE == kSwiGLU) out = silu(tot[0][v]) * tot[1][v];
+        if (MODE == kPlain && bias) out += bias[olrow];
+        if (yp) yp[o] = out;
+        if (ybp) ybp[o] = f32_to_bf16_rne(out);
+      }
+    }
+  };
+  mfp_stream<QT, DL, NR, W>(xr, chunks, my_tiles, make_rsrc(w0, 0u), tile_rsrc, emit, part);
 }
 
 template <int QT, bool DL, int MODE, int W>

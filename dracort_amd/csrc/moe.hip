@@ -46,7 +46,9 @@ struct MoeWs {
   int* assign_tok;  // [T*k] token of each assignment row, grouped by expert
   int* counts;      // [E]
   int* offsets;     // [E + 1]
-  float* h;         // [T*k, inter]  silu(gate) * up
+  float* h;         // [T*k, inter]  silu(gate) * up (register-core path)
+  uint16_t* hp;     // [3][T*k, inter] the same as three bf16 planes (matrix-core path)
+  size_t hp_plane;  // elements per plane: T*k*inter
   float* yk;        // [T*k, hidden] expert outputs
 };
 
@@ -68,6 +70,8 @@ static size_t moe_ws_layout(int64_t T, int64_t H, int64_t I, int E, int k, char*
   w.counts = (int*)take((size_t)E * 4);
   w.offsets = (int*)take((size_t)(E + 1) * 4);
   w.h = (float*)take(tk * (size_t)I * 4);
+  w.hp = (uint16_t*)take(3 * tk * (size_t)I * 2);
+  w.hp_plane = tk * (size_t)I;
   w.yk = (float*)take(tk * (size_t)H * 4);
   if (ws) *ws = w;
   return off;
@@ -240,7 +244,7 @@ __global__ __launch_bounds__(256) void moe_up_mfma_kernel(ExpertPtrs wg, ExpertP
                                         make_rsrc(wu.p[e], (uint32_t)I * row_bytes)};
   const int rowoff = (int)((uint32_t)(row0 + nl) * row_bytes);
   const size_t xstride = (size_t)H * (XBF16 ? 2 : 4);
-  for (int t0 = 0; t0 < cnt; t0 += 16) {
+  for (int t0 = 16 * (int)blockIdx.z; t0 < cnt; t0 += 16 * (int)gridDim.z) {
     const int mt = min(16, cnt - t0);
     // lanes of token rows past the expert's count repeat its last token
     const int tok = ws.assign_tok[off + t0 + min(nl, mt - 1)];
@@ -261,15 +265,76 @@ __global__ __launch_bounds__(256) void moe_up_mfma_kernel(ExpertPtrs wg, ExpertP
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int m = 4 * q + v;  // D layout: lane l holds token rows 4 (l / 16) + v, weight row l % 16
-        if (m < mt) ws.h[(size_t)(off + t0 + m) * I + row0 + nl] = silu_f(g[v]) * u[v];
+        if (m < mt) {
+          uint16_t a, b, c;
+          mf_split3(silu_f(g[v]) * u[v], a, b, c);
+          const size_t o = (size_t)(off + t0 + m) * I + row0 + nl;
+          ws.hp[o] = a;
+          ws.hp[ws.hp_plane + o] = b;
+          ws.hp[2 * ws.hp_plane + o] = c;
+        }
       }
     }
     __syncthreads();
   }
 }
 
+// Persistent form of the up projection for Q4_K experts with hidden <= 4096:
+// grid (workgroups per expert, experts); for each 16-token tile of its
+// expert a workgroup loads the gathered activations into registers once
+// (eight waves split the hidden dimension) and streams its share of the
+// gate/up row tiles against them (mfp_stream).
+__global__ __launch_bounds__(512) void moe_up_mfp_kernel(ExpertPtrs wg, ExpertPtrs wu,
+                                                         const uint16_t* __restrict__ x, int H, int I, MoeWs ws) {
+  constexpr int W = 8;
+  __shared__ mf_f32x4 part[2][W][2][64];
+  const int e = blockIdx.y;
+  const int cnt = ws.counts[e];
+  if (cnt == 0) return;
+  const int off = ws.offsets[e];
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, nl = lane & 15;
+  const int chunks = H >> 8;
+  const int ntiles = I >> 4;
+  const int my_tiles = ntiles > (int)blockIdx.x ? (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+  const int row_bytes = (H / 256) * 144;
+  const uint8_t* const gp = wg.p[e];
+  const uint8_t* const upp = wu.p[e];
+  uint16_t* const hp = ws.hp;
+  const size_t plane = ws.hp_plane;
+  const uint32_t mat_bytes = (uint32_t)I * (uint32_t)row_bytes;
+  for (int t0 = 16 * (int)blockIdx.z; t0 < cnt; t0 += 16 * (int)gridDim.z) {
+    const int mt = min(16, cnt - t0);
+    const int tok = ws.assign_tok[off + t0 + min(nl, mt - 1)];
+    typename MfpTypes<kQ4_K>::X xr[16 / W];
+    mfp_load_x<kQ4_K, W>(x + (size_t)tok * H, chunks, ks, q, xr);
+    auto tile_rsrc = [=](int i, int r) {
+      const int row = 16 * ((int)blockIdx.x + i * (int)gridDim.x);
+      return MfRow{make_rsrc(r == 0 ? gp : upp, mat_bytes), (row + nl) * row_bytes};
+    };
+    auto emit = [=](int i, const mf_f32x4 (&tot)[2]) {
+      const int col = 16 * ((int)blockIdx.x + i * (int)gridDim.x) + nl;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = 4 * q + v;  // D layout: lane l holds token rows 4 (l / 16) + v, weight row l % 16
+        if (m < mt) {
+          uint16_t a, b, c;
+          mf_split3(silu_f(tot[0][v]) * tot[1][v], a, b, c);
+          const size_t o = (size_t)(off + t0 + m) * I + col;
+          hp[o] = a;
+          hp[plane + o] = b;
+          hp[2 * plane + o] = c;
+        }
+      }
+    };
+    mfp_stream<kQ4_K, false, 2, W>(xr, chunks, my_tiles, make_rsrc(gp, 0u), tile_rsrc, emit, part);
+  }
+}
+
 // yk[off + t0 + m, :] = h[off + t0 + m, :] W_down[e]^T, 16 assignment rows per
-// pass (float32 h: three bf16 planes per MFMA group).
+// pass; h arrives as the three bf16 planes the up kernels wrote (three MFMAs
+// per group against exact codes, no split here).
 template <int QT>
 __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertPtrs wd, int H, int I, MoeWs ws) {
   __shared__ mf_f32x4 part[4][64];
@@ -284,11 +349,11 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertPtrs wd, int H
   const uint32_t row_bytes = (uint32_t)(I / Fmt<QT>::QK) * Fmt<QT>::BYTES;
   const __amdgpu_buffer_rsrc_t rs[1] = {make_rsrc(wd.p[e], (uint32_t)H * row_bytes)};
   const int rowoff = (int)((uint32_t)(row0 + nl) * row_bytes);
-  for (int t0 = 0; t0 < cnt; t0 += 16) {
+  for (int t0 = 16 * (int)blockIdx.z; t0 < cnt; t0 += 16 * (int)gridDim.z) {
     const int mt = min(16, cnt - t0);
-    const float* xrow = ws.h + (size_t)(off + t0 + min(nl, mt - 1)) * I;
+    const uint16_t* xrow = ws.hp + (size_t)(off + t0 + min(nl, mt - 1)) * I;
     mf_f32x4 acc[1] = {{0.f, 0.f, 0.f, 0.f}};
-    mf_accumulate<QT, false, 1>(rs, rowoff, xrow, q, ks, I >> 8, acc);
+    mf_accumulate<QT, false, 1, true>(rs, rowoff, xrow, q, ks, I >> 8, acc, ws.hp_plane);
     part[ks][lane] = acc[0];
     __syncthreads();
     if (ks == 0) {
@@ -335,14 +400,23 @@ static int launch_moe(const ExpertPtrs& wg, const ExpertPtrs& wu, const ExpertPt
     const int64_t up_bytes = (int64_t)I * (H / Fmt<QT>::QK) * Fmt<QT>::BYTES;
     const int64_t down_bytes = (int64_t)H * (I / Fmt<QT>::QK) * Fmt<QT>::BYTES;
     if (H % 256 == 0 && I % 256 == 0 && up_bytes < ((int64_t)1 << 31) && down_bytes < ((int64_t)1 << 31)) {
-      if (xbf16)
-        hipLaunchKernelGGL((moe_up_mfma_kernel<QT, true>), dim3((unsigned)(I / 16), (unsigned)E), dim3(256), 0, s,
+      // z: an expert's 16-token tiles side by side (an expert holds at most T
+      // tokens; slices past its count exit at once), so a crowded expert does
+      // not serialize its tiles
+      const unsigned zt = (unsigned)std::min((T + 15) / 16, 8);
+      if (QT == kQ4_K && xbf16 && H <= 4096) {
+        // one workgroup per CU, split evenly over the experts
+        const int per_expert = std::max(1, (device_cus() + E - 1) / E);
+        hipLaunchKernelGGL(moe_up_mfp_kernel, dim3((unsigned)per_expert, (unsigned)E, zt), dim3(512), 0, s, wg, wu,
+                           static_cast<const uint16_t*>(x), H, I, ws);
+      } else if (xbf16)
+        hipLaunchKernelGGL((moe_up_mfma_kernel<QT, true>), dim3((unsigned)(I / 16), (unsigned)E, zt), dim3(256), 0, s,
                            wg, wu, x, H, I, ws);
       else
-        hipLaunchKernelGGL((moe_up_mfma_kernel<QT, false>), dim3((unsigned)(I / 16), (unsigned)E), dim3(256), 0, s,
+        hipLaunchKernelGGL((moe_up_mfma_kernel<QT, false>), dim3((unsigned)(I / 16), (unsigned)E, zt), dim3(256), 0, s,
                            wg, wu, x, H, I, ws);
       if (int rc = check_launch("moe_up_mfma")) return rc;
-      hipLaunchKernelGGL((moe_down_mfma_kernel<QT>), dim3((unsigned)(H / 16), (unsigned)E), dim3(256), 0, s, wd, H,
+      hipLaunchKernelGGL((moe_down_mfma_kernel<QT>), dim3((unsigned)(H / 16), (unsigned)E, zt), dim3(256), 0, s, wd, H,
                          I, ws);
       if (int rc = check_launch("moe_down_mfma")) return rc;
       hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, s, y,

@@ -27,7 +27,8 @@ DRACO_EWORKSPACE = -5
 
 DRACO_DTYPE_F32 = 0
 DRACO_DTYPE_BF16 = 1
-DRACO_GGUF_Q6K_D_LAST = 0x100
+DRACO_GGUF_GGML_ORDER = 0x100  # Q2_K / Q3_K / Q6_K in upstream ggml field order
+DRACO_GGUF_Q6K_D_LAST = DRACO_GGUF_GGML_ORDER
 
 ABI_VERSION = 3
 

@@ -35,21 +35,29 @@ struct TypeInfo {
 };
 
 int decode_type(int ggml_type, TypeInfo* t) {
-  const int base = ggml_type & ~DRACO_GGUF_Q6K_D_LAST;
-  const bool d_last = (ggml_type & DRACO_GGUF_Q6K_D_LAST) != 0;
+  const int base = ggml_type & ~DRACO_GGUF_GGML_ORDER;
+  const bool d_last = (ggml_type & DRACO_GGUF_GGML_ORDER) != 0;
   switch (base) {
-    case kQ8_0: *t = {base, false, 32, 34}; break;
     case kQ4_0: *t = {base, false, 32, 18}; break;
+    case kQ4_1: *t = {base, false, 32, 20}; break;
+    case kQ5_0: *t = {base, false, 32, 22}; break;
+    case kQ5_1: *t = {base, false, 32, 24}; break;
+    case kQ8_0: *t = {base, false, 32, 34}; break;
+    case kQ8_K: *t = {base, false, 256, 258}; break;
+    case kQ2_K: *t = {base, d_last, 256, 84}; break;
+    case kQ3_K: *t = {base, d_last, 256, 110}; break;
     case kQ4_K: *t = {base, false, 256, 144}; break;
+    case kQ5_K: *t = {base, false, 256, 176}; break;
     case kQ6_K: *t = {base, d_last, 256, 210}; break;
     default:
       return set_error(DRACO_EINVAL_QTYPE,
-                       "GGUF quantization type %d is not supported by this build (supported: Q8_0=8, Q4_0=2, "
-                       "Q4_K=12, Q6_K=14)",
+                       "GGUF quantization type %d is not supported by this build (supported: Q4_0=2, Q4_1=3, "
+                       "Q5_0=6, Q5_1=7, Q8_0=8, Q2_K=10, Q3_K=11, Q4_K=12, Q5_K=13, Q6_K=14, Q8_K=15)",
                        ggml_type);
   }
-  if (d_last && base != kQ6_K)
-    return set_error(DRACO_EINVAL_QTYPE, "layout flag DRACO_GGUF_Q6K_D_LAST only applies to Q6_K (got type %d)",
+  if (d_last && base != kQ2_K && base != kQ3_K && base != kQ6_K)
+    return set_error(DRACO_EINVAL_QTYPE,
+                     "layout flag DRACO_GGUF_GGML_ORDER only applies to Q2_K, Q3_K and Q6_K (got type %d)",
                      ggml_type);
   return DRACO_OK;
 }

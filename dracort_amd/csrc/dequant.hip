@@ -1,18 +1,26 @@
 // Bit-exact GGUF block dequantization to float32 for gfx950.
 //
 // Replaces the reference's _dequantize (draco/format/gguf.py:272-497) for
-// Q8_0 (:300-303), Q4_0 (:310-316), Q4_K (:425-468) and Q6_K (:470-495).
-// The float32 rounding sequence is the reference's:
+// Q8_0 (:300-303), Q8_K (:305-308), Q4_0 (:310-316), Q4_1 (:318-324),
+// Q5_0 / Q5_1 (:326-353), Q2_K (:355-374), Q3_K (:376-423), Q4_K / Q5_K
+// (:425-468) and Q6_K (:470-495).  The float32 rounding sequence is the
+// reference's:
 //   Q8_0  fl(q * d)                 Q4_0  fl((q - 8) * d)
 //   Q4_K  fl(fl(fl(d*sc) * q) - fl(dmin*m))
 //   Q6_K  fl(fl(d*sc) * (q - 32))
 // so this translation unit is compiled with -ffp-contract=off and each kernel
 // body also disables contraction: an FMA would skip one of the roundings.
+// Q4_1 / Q5_1 / Q2_K / Q5_K compute a*code + b with an explicit fmaf, where a
+// and b are exact float32 products of the block's float16 and integer scales:
+// the reference rounds that same exact value once (Q4_1 / Q5_1 add m to an
+// exact product in float32; Q2_K / Q5_K form it in float64 and round it to
+// float32 on the way to the kernel), and so does the FMA.  Q5_0 / Q8_K / Q3_K
+// are exact products (code - c) * scale, as in the reference.
 //
 // One thread decodes one 32-weight unit (see gguf_common.h) and writes it with
 // 16-byte stores; the kernel is bound by the float32 write stream (~7x the
 // packed read for Q4_K).
-#include "gguf_common.h"
+#include "gemv_core.h"
 #include "draco_internal.h"
 
 namespace draco {
@@ -78,6 +86,30 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
         st4(p + 4 * j, v[0], v[1], v[2], v[3]);
       }
     }
+  } else if constexpr (QT != kQ6_K) {
+    // Q4_1 Q5_1 Q2_K Q5_K: w = fma(a, code, b), one rounding.  Q8_K Q5_0 Q3_K
+    // (no separate offset): w = a * (code - c), exact, which also keeps the
+    // reference's sign of zero (-0 for a zero code times a negative scale;
+    // an FMA whose two terms cancel gives +0).
+    constexpr int G = Fmt<QT>::G, GL = Fmt<QT>::GL;
+    constexpr bool SYM = QT == kQ8_K || QT == kQ5_0 || QT == kQ3_K;
+    constexpr float C = QT == kQ5_0 ? 16.f : (QT == kQ3_K ? 4.f : 0.f);
+    float a[G], b[G];
+    unit_coeffs<QT>(r, u, a, b);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float* p = o + group_pos<QT>(u, g);
+#pragma unroll
+      for (int j = 0; j < GL / 4; ++j) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float c = unit_code<QT>(r, g, 4 * j + i, u);
+          v[i] = SYM ? (c - C) * a[g] : fmaf(a[g], c, b[g]);
+        }
+        st4(p + 4 * j, v[0], v[1], v[2], v[3]);
+      }
+    }
   } else {  // Q6_K
     const float d = f16_bits_to_f32(r.d);
     const int l16 = ((u & 7) & 3) >> 1;  // l0 / 16
@@ -115,7 +147,18 @@ int dequant_dispatch(int qtype, bool d_last, const void* w, float* out, int64_t 
   switch (qtype) {
     case kQ8_0: return launch_dequant<kQ8_0, false>(p, out, n_rows, k, s);
     case kQ4_0: return launch_dequant<kQ4_0, false>(p, out, n_rows, k, s);
+    case kQ4_1: return launch_dequant<kQ4_1, false>(p, out, n_rows, k, s);
+    case kQ5_0: return launch_dequant<kQ5_0, false>(p, out, n_rows, k, s);
+    case kQ5_1: return launch_dequant<kQ5_1, false>(p, out, n_rows, k, s);
+    case kQ8_K: return launch_dequant<kQ8_K, false>(p, out, n_rows, k, s);
     case kQ4_K: return launch_dequant<kQ4_K, false>(p, out, n_rows, k, s);
+    case kQ5_K: return launch_dequant<kQ5_K, false>(p, out, n_rows, k, s);
+    case kQ2_K:
+      return d_last ? launch_dequant<kQ2_K, true>(p, out, n_rows, k, s)
+                    : launch_dequant<kQ2_K, false>(p, out, n_rows, k, s);
+    case kQ3_K:
+      return d_last ? launch_dequant<kQ3_K, true>(p, out, n_rows, k, s)
+                    : launch_dequant<kQ3_K, false>(p, out, n_rows, k, s);
     case kQ6_K:
       return d_last ? launch_dequant<kQ6_K, true>(p, out, n_rows, k, s)
                     : launch_dequant<kQ6_K, false>(p, out, n_rows, k, s);

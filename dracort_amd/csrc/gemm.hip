@@ -35,7 +35,7 @@ constexpr int kBK = 64;
 constexpr int kLDK = kBK + 8;  // padded LDS row (bf16 elements): 16-byte aligned, conflict-free
 
 template <int QT> struct GemmCfg {
-  static constexpr int UR = (QT == kQ6_K) ? 4 : 2;  // 32-weight units touched per row per K step
+  static constexpr int UR = (Fmt<QT>::FAM == kFamK6) ? 4 : 2;  // 32-weight units touched per row per K step
   static constexpr int UPT = kBN * UR / 256;        // units per thread
   static constexpr int APT = kBM * kBK / 8 / 256;   // 16-byte x pieces per thread
 };
@@ -43,14 +43,14 @@ template <int QT> struct GemmCfg {
 // Unit index of the ur-th unit touched by the K window starting at k0.
 template <int QT>
 __device__ __forceinline__ int window_unit(int k0, int ur) {
-  if constexpr (QT == kQ6_K) return 8 * (k0 >> 8) + 4 * ((k0 >> 7) & 1) + ur;
+  if constexpr (Fmt<QT>::FAM == kFamK6) return 8 * (k0 >> 8) + 4 * ((k0 >> 7) & 1) + ur;
   return (k0 >> 5) + ur;
 }
 
 // Whether group g of a unit lies in the 64-wide window starting at k0.
 template <int QT>
 __device__ __forceinline__ bool group_in_window(int k0, int g) {
-  if constexpr (QT == kQ6_K) return (g >> 1) == ((k0 >> 6) & 1);
+  if constexpr (Fmt<QT>::FAM == kFamK6) return (g >> 1) == ((k0 >> 6) & 1);
   return true;
 }
 
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ w
             uint32_t h[2], md[2], l[2];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-              const float wv = live ? fmaf(a[g], unit_code<QT>(breg[i], g, e8 + e + t), b[g]) : 0.f;
+              const float wv = live ? fmaf(a[g], unit_code<QT>(breg[i], g, e8 + e + t, u), b[g]) : 0.f;
               h[t] = bf16_rne_bits(wv);
               const float r1 = wv - __uint_as_float(h[t] << 16);
               md[t] = bf16_rne_bits(r1);
@@ -224,7 +224,18 @@ int gemm_dispatch(int qtype, bool d_last, const void* w, const void* x, const fl
   switch (qtype) {
     case kQ8_0: return launch_gemm<kQ8_0, false>(w, x, bias, y, m, n, k, s);
     case kQ4_0: return launch_gemm<kQ4_0, false>(w, x, bias, y, m, n, k, s);
+    case kQ4_1: return launch_gemm<kQ4_1, false>(w, x, bias, y, m, n, k, s);
+    case kQ5_0: return launch_gemm<kQ5_0, false>(w, x, bias, y, m, n, k, s);
+    case kQ5_1: return launch_gemm<kQ5_1, false>(w, x, bias, y, m, n, k, s);
+    case kQ8_K: return launch_gemm<kQ8_K, false>(w, x, bias, y, m, n, k, s);
     case kQ4_K: return launch_gemm<kQ4_K, false>(w, x, bias, y, m, n, k, s);
+    case kQ5_K: return launch_gemm<kQ5_K, false>(w, x, bias, y, m, n, k, s);
+    case kQ2_K:
+      return d_last ? launch_gemm<kQ2_K, true>(w, x, bias, y, m, n, k, s)
+                    : launch_gemm<kQ2_K, false>(w, x, bias, y, m, n, k, s);
+    case kQ3_K:
+      return d_last ? launch_gemm<kQ3_K, true>(w, x, bias, y, m, n, k, s)
+                    : launch_gemm<kQ3_K, false>(w, x, bias, y, m, n, k, s);
     case kQ6_K:
       return d_last ? launch_gemm<kQ6_K, true>(w, x, bias, y, m, n, k, s)
                     : launch_gemm<kQ6_K, false>(w, x, bias, y, m, n, k, s);

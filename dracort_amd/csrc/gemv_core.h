@@ -93,13 +93,16 @@ __device__ __forceinline__ void load_x(const void* __restrict__ xr, int p, float
 // Per-group coefficients a[g], b[g] with w = a*code + b.
 template <int QT>
 __device__ __forceinline__ void unit_coeffs(const Raw<QT>& r, int u, float* a, float* b) {
-  if constexpr (QT == kQ8_0) {
+  if constexpr (QT == kQ8_0 || QT == kQ8_K) {
     a[0] = f16_bits_to_f32(r.d);
     b[0] = 0.f;
-  } else if constexpr (QT == kQ4_0) {
+  } else if constexpr (QT == kQ4_0 || QT == kQ5_0) {
     a[0] = f16_bits_to_f32(r.d);
-    b[0] = -8.f * a[0];
-  } else if constexpr (QT == kQ4_K) {
+    b[0] = (QT == kQ4_0 ? -8.f : -16.f) * a[0];
+  } else if constexpr (QT == kQ4_1 || QT == kQ5_1) {
+    a[0] = f16_bits_to_f32(r.dm);
+    b[0] = f16_bits_to_f32(r.dm >> 16);
+  } else if constexpr (Fmt<QT>::FAM == kFamK4) {
     // all eight 6-bit scales / mins as bytes (SWAR form of the reference's
     // _scale_min), then this unit's two sub-blocks j0, j0 + 1 by byte select
     const float d = f16_bits_to_f32(r.head.x), dmin = f16_bits_to_f32(r.head.x >> 16);
@@ -114,6 +117,31 @@ __device__ __forceinline__ void unit_coeffs(const Raw<QT>& r, int u, float* a, f
       a[g] = d * (float)((scw >> (sh + 8 * g)) & 0xFFu);
       b[g] = -(dmin * (float)((mw >> (sh + 8 * g)) & 0xFFu));
     }
+  } else if constexpr (QT == kQ2_K) {
+    // scale byte of group t: sc[8*half + 2*t + sub], low nibble scale, high nibble min
+    const float d = f16_bits_to_f32(r.dm), dmin = f16_bits_to_f32(r.dm >> 16);
+    const int sub = ((u & 7) >> 1) & 1;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t byte = (r.sc[t >> 1] >> (8 * (2 * (t & 1) + sub))) & 0xFFu;
+      a[t] = d * (float)(byte & 0x0Fu);
+      b[t] = -(dmin * (float)(byte >> 4));
+    }
+  } else if constexpr (QT == kQ3_K) {
+    // 6-bit scale 8*half + 2*t + sub: low nibble from byte (2t + sub) % 8
+    // (nibble `half`), top two bits from byte 8 + (2t + sub) % 4 (bits
+    // 2*(2*half + t/2)); built as the two scale words of this half
+    const float d = f16_bits_to_f32(r.d);
+    const int half = (u & 7) >> 2, sub = ((u & 7) >> 1) & 1;
+    const int nsh = 4 * half;
+    const uint32_t wa = ((r.s12[0] >> nsh) & 0x0F0F0F0Fu) | (((r.s12[2] >> nsh) & 0x03030303u) << 4);
+    const uint32_t wb = ((r.s12[1] >> nsh) & 0x0F0F0F0Fu) | (((r.s12[2] >> (nsh + 2)) & 0x03030303u) << 4);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t sc = ((t < 2 ? wa : wb) >> (8 * (2 * (t & 1) + sub))) & 0xFFu;
+      a[t] = d * (float)((int)sc - 32);
+      b[t] = -4.f * a[t];
+    }
   } else {
     const float d = f16_bits_to_f32(r.d);
     const int l16 = ((u & 7) & 3) >> 1;
@@ -127,37 +155,54 @@ __device__ __forceinline__ void unit_coeffs(const Raw<QT>& r, int u, float* a, f
   }
 }
 
-// Code of element i (0..GL-1) of group g as float.
-template <int QT>
-__device__ __forceinline__ float unit_code(const Raw<QT>& r, int g, int i) {
-  if constexpr (QT == kQ8_0) {
-    return sbyte_f(r.q[i >> 2], i & 3);
-  } else if constexpr (QT == kQ4_0) {
-    return i < 16 ? ubyte_f(nib_lo(r.q[i >> 2]), i & 3) : ubyte_f(nib_hi(r.q[(i - 16) >> 2]), i & 3);
-  } else if constexpr (QT == kQ4_K) {
-    const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
-    return ubyte_f(g == 0 ? nib_lo(q[i >> 2]) : nib_hi(q[i >> 2]), i & 3);
-  } else {
-    const int h = i >> 2;
-    return ubyte_f(q6_codes(g, r.qla[h], r.qlb[h], r.qh[h]), i & 3);
-  }
-}
+// Four 1-bit fields (bits 0..3 of x) spread to bit 0 of each byte.
+__device__ __forceinline__ uint32_t spread4(uint32_t x) { return ((x & 0xFu) * 0x00204081u) & 0x01010101u; }
 
 // Dword j (codes 4j .. 4j+3, one per byte) of group g, unsigned codes only.
+// `u` is the unit index (Q5_K and Q3_K select their high-bit plane by it).
 template <int QT>
-__device__ __forceinline__ uint32_t unit_code_dword(const Raw<QT>& r, int g, int j) {
-  if constexpr (QT == kQ4_0) {
+__device__ __forceinline__ uint32_t unit_code_dword(const Raw<QT>& r, int g, int j, int u) {
+  if constexpr (QT == kQ4_0 || QT == kQ4_1) {
     return j < 4 ? nib_lo(r.q[j]) : nib_hi(r.q[j - 4]);
+  } else if constexpr (QT == kQ5_0 || QT == kQ5_1) {
+    const uint32_t n = j < 4 ? nib_lo(r.q[j]) : nib_hi(r.q[j - 4]);
+    return n | (spread4(r.qh >> (4 * j)) << 4);
   } else if constexpr (QT == kQ4_K) {
     const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
     return g == 0 ? nib_lo(q[j]) : nib_hi(q[j]);
+  } else if constexpr (QT == kQ5_K) {
+    // fifth bit of sub-block 2*((u & 7) >> 1) + g is bit (that index) of qh[l]
+    const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+    const uint32_t h[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+    const int bit = 2 * ((u & 7) >> 1) + g;
+    return (g == 0 ? nib_lo(q[j]) : nib_hi(q[j])) | (((h[j] >> bit) & 0x01010101u) << 4);
+  } else if constexpr (QT == kQ2_K) {
+    return (r.qs[j] >> (2 * g)) & 0x03030303u;
+  } else if constexpr (QT == kQ3_K) {
+    const int half = (u & 7) >> 2;
+    return ((r.qs[j] >> (2 * g)) & 0x03030303u) | (((r.hm[j] >> (4 * half + g)) & 0x01010101u) << 2);
   } else {
     return q6_codes(g, r.qla[j], r.qlb[j], r.qh[j]);
   }
 }
 
-// Formats whose codes are small unsigned integers (bf16 dot2 path).
-template <int QT> struct UnsignedCodes { static constexpr bool value = QT != kQ8_0; };
+// Code of element i (0..GL-1) of group g as float.
+template <int QT>
+__device__ __forceinline__ float unit_code(const Raw<QT>& r, int g, int i, int u) {
+  if constexpr (QT == kQ8_0 || QT == kQ8_K) {
+    return sbyte_f(r.q[i >> 2], i & 3);
+  } else {
+    return ubyte_f(unit_code_dword<QT>(r, g, i >> 2, u), i & 3);
+  }
+}
+
+// Formats on the bf16 dot2 path: unsigned codes carried as bf16 128 + code
+// (one byte permute per pair), the 128 taken back out through the group's
+// activation sum.  That cancellation costs log2(128 / max code) bits, so the
+// 2- and 3-bit formats (Q2_K, Q3_K) take the float32 FMA path instead.
+template <int QT> struct UnsignedCodes {
+  static constexpr bool value = Fmt<QT>::OFF && QT != kQ2_K && QT != kQ3_K;
+};
 
 // acc[r][mi] (lane partial sums) for rows n0 .. n0+R-1 and activation rows
 // 0 .. m-1 (m <= MT); xrow(mi) returns the address of activation row mi.
@@ -192,7 +237,7 @@ __device__ __forceinline__ void gemv_accumulate(const uint8_t* __restrict__ w, i
           float xv[GL];
           load_x<GL, XBF16>(xr, group_pos<QT>(u, g), xv);
           float xsum = 0.f;
-          if constexpr (QT != kQ8_0) {
+          if constexpr (F::OFF) {
 #pragma unroll
             for (int i = 0; i < GL; ++i) xsum += xv[i];
           }
@@ -200,9 +245,9 @@ __device__ __forceinline__ void gemv_accumulate(const uint8_t* __restrict__ w, i
           for (int r = 0; r < R; ++r) {
             float dot = 0.f;
 #pragma unroll
-            for (int i = 0; i < GL; ++i) dot = fmaf(unit_code<QT>(raw[r], g, i), xv[i], dot);
+            for (int i = 0; i < GL; ++i) dot = fmaf(unit_code<QT>(raw[r], g, i, u), xv[i], dot);
             acc[r][mi] = fmaf(a[r][g], dot, acc[r][mi]);
-            if constexpr (QT != kQ8_0) acc[r][mi] = fmaf(b[r][g], xsum, acc[r][mi]);
+            if constexpr (F::OFF) acc[r][mi] = fmaf(b[r][g], xsum, acc[r][mi]);
           }
         }
       }
@@ -251,11 +296,11 @@ __device__ __forceinline__ int perm_slot_of_chunk(int c) {
   constexpr int CE = XChunk<XBF16>::CE;
   const int p = c * CE;  // natural element offset within the 2048-element step
   int l, e;              // unit (= lane) and element index within the unit's G * GL activations
-  if constexpr (QT == kQ4_K) {
+  if constexpr (Fmt<QT>::FAM == kFamK4) {
     const int q = p & 255;
     l = 8 * (p >> 8) + 2 * (q >> 6) + ((q >> 4) & 1);
     e = 16 * ((q >> 5) & 1) + (q & 15);
-  } else if constexpr (QT == kQ6_K) {
+  } else if constexpr (Fmt<QT>::FAM == kFamK6) {
     const int q = p & 255;
     l = 8 * (p >> 8) + 4 * (q >> 7) + ((q >> 3) & 3);
     e = 8 * ((q >> 5) & 3) + (q & 7);
@@ -356,7 +401,7 @@ __device__ __forceinline__ void unit_math_lds(const Raw<QT> (&raw)[R], int u, in
       for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int j = 0; j < GL / 4; ++j) {
-          const uint32_t c = unit_code_dword<QT>(raw[r], g, j);
+          const uint32_t c = unit_code_dword<QT>(raw[r], g, j, u);
           cp[r][g][2 * j] = code_pair_lo(c);
           cp[r][g][2 * j + 1] = code_pair_hi(c);
         }
@@ -431,7 +476,7 @@ __device__ __forceinline__ void unit_math_lds(const Raw<QT> (&raw)[R], int u, in
             load_x<GL, false>(reinterpret_cast<const float*>(xs) + (size_t)mi * k, group_pos<QT>(u, g), xv);
           }
           float xsum_g = 0.f;
-          if constexpr (QT != kQ8_0) {
+          if constexpr (F::OFF) {
             if constexpr (XPRE) {
               xsum_g = xsum[((size_t)mi * units + u) * G + g];
             } else {
@@ -443,9 +488,9 @@ __device__ __forceinline__ void unit_math_lds(const Raw<QT> (&raw)[R], int u, in
           for (int r = 0; r < R; ++r) {
             float dot = 0.f;
 #pragma unroll
-            for (int i = 0; i < GL; ++i) dot = fmaf(unit_code<QT>(raw[r], g, i), xv[i], dot);
+            for (int i = 0; i < GL; ++i) dot = fmaf(unit_code<QT>(raw[r], g, i, u), xv[i], dot);
             acc[r][mi] = fmaf(a[r][g], dot, acc[r][mi]);
-            if constexpr (QT != kQ8_0) acc[r][mi] = fmaf(b[r][g], xsum_g, acc[r][mi]);
+            if constexpr (F::OFF) acc[r][mi] = fmaf(b[r][g], xsum_g, acc[r][mi]);
           }
         }
       }

@@ -305,7 +305,14 @@ inline int64_t row_bytes_of(int qtype, int k) {
   switch (qtype) {
     case kQ8_0: return (int64_t)(k / 32) * 34;
     case kQ4_0: return (int64_t)(k / 32) * 18;
+    case kQ4_1: return (int64_t)(k / 32) * 20;
+    case kQ5_0: return (int64_t)(k / 32) * 22;
+    case kQ5_1: return (int64_t)(k / 32) * 24;
+    case kQ8_K: return (int64_t)(k / 256) * 258;
+    case kQ2_K: return (int64_t)(k / 256) * 84;
+    case kQ3_K: return (int64_t)(k / 256) * 110;
     case kQ4_K: return (int64_t)(k / 256) * 144;
+    case kQ5_K: return (int64_t)(k / 256) * 176;
     default: return (int64_t)(k / 256) * 210;
   }
 }
@@ -374,6 +381,44 @@ static int stream_mt(const StreamJob& job, hipStream_t s) {
   return launch_stream_x<QT, DL, 16, XBF16, MODE>(job, s);
 }
 
+// Q4_1 Q5_0 Q5_1 Q8_K Q2_K Q3_K Q5_K: the same streaming kernel with fewer
+// activation-row tiles (1, 4, 16), one translation unit per mode
+// (gemv_ext_*.hip) so they compile in parallel with the rest.
+int stream_ext_plain(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s);
+int stream_ext_swiglu(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s);
+int stream_ext_resid(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s);
+
+template <int QT, bool DL, int MODE, bool XBF16>
+static int stream_mt_ext(const StreamJob& job, hipStream_t s) {
+  if (job.m <= 1) return launch_stream_x<QT, DL, 1, XBF16, MODE>(job, s);
+  if (job.m <= 4) return launch_stream_x<QT, DL, 4, XBF16, MODE>(job, s);
+  return launch_stream_x<QT, DL, 16, XBF16, MODE>(job, s);
+}
+
+template <int MODE>
+static int stream_ext_dispatch(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s) {
+#define DRACO_EXT_CASE(QT)                                                                      \
+  case QT:                                                                                      \
+    return xbf16 ? stream_mt_ext<QT, false, MODE, true>(job, s) : stream_mt_ext<QT, false, MODE, false>(job, s);
+#define DRACO_EXT_CASE_DL(QT)                                                                   \
+  case QT:                                                                                      \
+    if (d_last)                                                                                 \
+      return xbf16 ? stream_mt_ext<QT, true, MODE, true>(job, s) : stream_mt_ext<QT, true, MODE, false>(job, s); \
+    return xbf16 ? stream_mt_ext<QT, false, MODE, true>(job, s) : stream_mt_ext<QT, false, MODE, false>(job, s);
+  switch (qtype) {
+    DRACO_EXT_CASE(kQ4_1)
+    DRACO_EXT_CASE(kQ5_0)
+    DRACO_EXT_CASE(kQ5_1)
+    DRACO_EXT_CASE(kQ8_K)
+    DRACO_EXT_CASE(kQ5_K)
+    DRACO_EXT_CASE_DL(kQ2_K)
+    DRACO_EXT_CASE_DL(kQ3_K)
+    default: return set_error(DRACO_EINVAL_QTYPE, "unsupported ggml type %d", qtype);
+  }
+#undef DRACO_EXT_CASE
+#undef DRACO_EXT_CASE_DL
+}
+
 template <int MODE>
 static int stream_dispatch(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s) {
   switch (qtype) {
@@ -384,7 +429,10 @@ static int stream_dispatch(int qtype, bool d_last, const StreamJob& job, bool xb
       if (d_last)
         return xbf16 ? stream_mt<kQ6_K, true, MODE, true>(job, s) : stream_mt<kQ6_K, true, MODE, false>(job, s);
       return xbf16 ? stream_mt<kQ6_K, false, MODE, true>(job, s) : stream_mt<kQ6_K, false, MODE, false>(job, s);
-    default: return set_error(DRACO_EINVAL_QTYPE, "unsupported ggml type %d", qtype);
+    default:
+      if constexpr (MODE == kPlain) return stream_ext_plain(qtype, d_last, job, xbf16, s);
+      if constexpr (MODE == kSwiGLU) return stream_ext_swiglu(qtype, d_last, job, xbf16, s);
+      return stream_ext_resid(qtype, d_last, job, xbf16, s);
   }
 }
 

@@ -454,7 +454,7 @@ extern "C" int draco_gguf_moe_ffn(int ggml_type, const void* const* w_gate, cons
                                   int n_experts, int top_k, void* workspace, size_t workspace_bytes, void* stream) {
   int qk = 0, bb = 0;
   if (int rc = draco_gguf_block_info(ggml_type, &qk, &bb)) return rc;
-  if (ggml_type & DRACO_GGUF_Q6K_D_LAST)
+  if (ggml_type & DRACO_GGUF_GGML_ORDER)
     return set_error(DRACO_EINVAL_QTYPE, "MoE experts take reference-layout blocks only");
   if (n_experts < 1 || n_experts > kMaxExperts)
     return set_error(DRACO_EINVAL_SHAPE, "n_experts must be in 1..%d, got %d", kMaxExperts, n_experts);
@@ -495,7 +495,15 @@ extern "C" int draco_gguf_moe_ffn(int ggml_type, const void* const* w_gate, cons
   switch (ggml_type) {
     case kQ8_0: return launch_moe<kQ8_0>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
     case kQ4_0: return launch_moe<kQ4_0>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+    case kQ4_1: return launch_moe<kQ4_1>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+    case kQ5_0: return launch_moe<kQ5_0>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+    case kQ5_1: return launch_moe<kQ5_1>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+    case kQ8_K: return launch_moe<kQ8_K>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+    case kQ2_K: return launch_moe<kQ2_K>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+    case kQ3_K: return launch_moe<kQ3_K>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
     case kQ4_K: return launch_moe<kQ4_K>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
-    default: return launch_moe<kQ6_K>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+    case kQ5_K: return launch_moe<kQ5_K>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+    case kQ6_K: return launch_moe<kQ6_K>(wg, wu, wd, router_logits, x, xbf16, y, T, H, I, n_experts, top_k, ws, s);
+    default: return set_error(DRACO_EINVAL_QTYPE, "unsupported ggml type %d", ggml_type);
   }
 }

@@ -16,11 +16,11 @@ dequantizes it to float32 on first use (``draco/format/gguf.py:812-834``),
 this reader hands out the packed payload itself -- a read-only view of the
 mapping -- so the uploader can stream it into HBM in its native layout.
 
-Q6_K field order.  The reference decodes Q6_K blocks with ``d`` in the first
-two bytes (``draco/format/gguf.py:471-474``); upstream ggml files store it in
-the last two.  ``q6k_layout="reference"`` (default) reads blocks as the
-reference does; ``q6k_layout="ggml"`` tags Q6_K tensors with the kernels'
-``Q6K_D_LAST`` layout flag instead.
+Field order.  The reference decodes Q2_K, Q3_K and Q6_K blocks with their
+float16 scales first (``draco/format/gguf.py:355-359, 376-380, 470-474``);
+upstream ggml files store them last.  ``field_order="reference"`` (default)
+reads blocks as the reference does; ``field_order="ggml"`` tags Q2_K / Q3_K /
+Q6_K tensors with the kernels' ``GGML_ORDER`` layout flag instead.
 """
 
 from __future__ import annotations
@@ -34,7 +34,7 @@ from typing import Any, Dict, Iterator, List, Optional, Tuple
 import numpy as np
 
 from dracort_amd.exceptions import DracoFormatError
-from dracort_amd.format.gguf import GGML_TYPE_Q6_K, Q6K_D_LAST, GgufTensorInfo
+from dracort_amd.format.gguf import GGML_ORDER, ORDER_TYPES, GgufTensorInfo
 
 GGUF_MAGIC = b"GGUF"
 
@@ -109,7 +109,7 @@ def tensor_nbytes(ggml_type: int, n_elements: int, name: str = "") -> int:
 @dataclass
 class GGUFTensor:
     """Directory entry: ``info`` (shape, absolute offset, bytes) plus the
-    ggml type the kernels take (Q6_K tagged with its field order)."""
+    ggml type the kernels take (Q2_K / Q3_K / Q6_K tagged with their field order)."""
 
     info: GgufTensorInfo
     kernel_type: int
@@ -130,11 +130,11 @@ class GGUFTensor:
 class GGUFFile:
     """Opens and maps a ``.gguf`` file; ``payload(name)`` is zero-copy."""
 
-    def __init__(self, path: str, q6k_layout: str = "reference") -> None:
-        if q6k_layout not in ("reference", "ggml"):
-            raise ValueError(f"q6k_layout must be 'reference' or 'ggml', got {q6k_layout!r}")
+    def __init__(self, path: str, field_order: str = "reference") -> None:
+        if field_order not in ("reference", "ggml"):
+            raise ValueError(f"field_order must be 'reference' or 'ggml', got {field_order!r}")
         self.path = path
-        self.q6k_layout = q6k_layout
+        self.field_order = field_order
         self._file = open(path, "rb")
         self._map: Optional[mmap.mmap] = None
         try:
@@ -189,7 +189,7 @@ class GGUFFile:
                 info = GgufTensorInfo(name=name, ggml_type=ttype, shape=tuple(reversed(dims)), offset=off,
                                       nbytes=nbytes, alignment=align,
                                       dtype=FLOAT_TYPES[ttype][0] if ttype in FLOAT_TYPES else "f32")
-                ktype = ttype | Q6K_D_LAST if (ttype == GGML_TYPE_Q6_K and q6k_layout == "ggml") else ttype
+                ktype = ttype | GGML_ORDER if (ttype in ORDER_TYPES and field_order == "ggml") else ttype
                 self._tensors[name] = GGUFTensor(info, ktype)
         except Exception:
             self.close()

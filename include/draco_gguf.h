@@ -21,8 +21,12 @@
  *    (a truncated payload) is rejected with DRACO_EINVAL_SHAPE before any
  *    launch.
  *  - ggml_type is the GGUF type id, optionally OR-ed with
- *    DRACO_GGUF_Q6K_D_LAST for Q6_K blocks stored in upstream ggml field order
- *    (ql, qh, scales, d) instead of the reference's (d, ql, qh, scales).
+ *    DRACO_GGUF_GGML_ORDER for Q2_K / Q3_K / Q6_K blocks stored in upstream
+ *    ggml field order instead of the reference's, which puts the float16
+ *    scales first:
+ *      Q2_K  reference d, dmin, qs[64], scales[16]   ggml scales, qs, d, dmin
+ *      Q3_K  reference d, scales[12], qs[64], hmask  ggml hmask, qs, scales, d
+ *      Q6_K  reference d, ql, qh, scales[16]         ggml ql, qh, scales, d
  */
 #ifndef DRACO_GGUF_H
 #define DRACO_GGUF_H
@@ -34,13 +38,23 @@
 extern "C" {
 #endif
 
-/* GGUF type ids handled here (reference: draco/format/gguf.py:57-72). */
+/* GGUF type ids handled here: every block type of the reference's
+ * _BLOCK_LAYOUTS (reference: draco/format/gguf.py:57-87). */
 #define DRACO_GGML_TYPE_Q4_0 2
+#define DRACO_GGML_TYPE_Q4_1 3
+#define DRACO_GGML_TYPE_Q5_0 6
+#define DRACO_GGML_TYPE_Q5_1 7
 #define DRACO_GGML_TYPE_Q8_0 8
+#define DRACO_GGML_TYPE_Q2_K 10
+#define DRACO_GGML_TYPE_Q3_K 11
 #define DRACO_GGML_TYPE_Q4_K 12
+#define DRACO_GGML_TYPE_Q5_K 13
 #define DRACO_GGML_TYPE_Q6_K 14
-/* Layout flag: Q6_K field order of upstream ggml (d stored last). */
-#define DRACO_GGUF_Q6K_D_LAST 0x100
+#define DRACO_GGML_TYPE_Q8_K 15
+/* Layout flag: upstream ggml field order of Q2_K / Q3_K / Q6_K blocks. */
+#define DRACO_GGUF_GGML_ORDER 0x100
+/* Older name of the same flag (it first applied to Q6_K only). */
+#define DRACO_GGUF_Q6K_D_LAST DRACO_GGUF_GGML_ORDER
 
 /* Activation dtypes. */
 #define DRACO_DTYPE_F32 0

@@ -17,8 +17,20 @@ from dracort_amd.quantization import quantize
 from oracle import gguf_ref, matmul_ref
 
 Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
+Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K, Q8_K = 3, 6, 7, 10, 11, 13, 15
+GGML_ORDER = 0x100
 TYPES = [Q8_0, Q4_0, Q4_K, Q6_K]
-NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+MORE_TYPES = [Q4_1, Q5_0, Q5_1, Q8_K, Q2_K, Q3_K, Q5_K]
+NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1",
+         Q2_K: "Q2_K", Q3_K: "Q3_K", Q5_K: "Q5_K", Q8_K: "Q8_K"}
+
+
+def qk_of(qtype: int) -> int:
+    return gguf_ref.BLOCK_LAYOUT[qtype & ~GGML_ORDER][0]
+
+
+def type_name(qtype: int) -> str:
+    return NAMES[qtype & ~GGML_ORDER] + ("/ggml-order" if qtype & GGML_ORDER else "")
 TOL = 1e-3  # max elementwise relative error vs the fp64 closed form (floor 1e-3 * max|ref|)
 
 
@@ -36,7 +48,7 @@ def quantized(qtype: int, n: int, k: int, seed: int = 0):
     w = synth_weight(n, k, seed)
     blocks = quantize(torch.from_numpy(w), qtype).numpy()
     base = qtype & ~0x100
-    return blocks, gguf_ref.dequantize_matrix(base, blocks, (n, k), q6k_d_last=bool(qtype & 0x100))
+    return blocks, gguf_ref.dequantize_matrix(base, blocks, (n, k), ggml_order=bool(qtype & 0x100))
 
 
 def activations(m: int, k: int, seed: int, dtype: torch.dtype) -> torch.Tensor:

@@ -1,6 +1,6 @@
 """GGUF container reader (host side): metadata of every value type, tensor
 directory (reversed dims, aligned data section, absolute offsets), zero-copy
-payloads, the Q6_K layout tag, and the reference's rejection cases
+payloads, the Q2_K / Q3_K / Q6_K field-order tag, and the reference's rejection cases
 (bad magic / version / alignment, tensors past the end, partial blocks)."""
 
 import os
@@ -35,11 +35,15 @@ def _tensors():
     q4k = quantize(w, 12).numpy().tobytes()
     q6k = quantize(w[:4], 14).numpy().tobytes()
     q80 = quantize(w[:3, :64], 8).numpy().tobytes()
+    q3k = quantize(w[:2], 11).numpy().tobytes()
+    q51 = quantize(w[:5, :96], 7).numpy().tobytes()
     norm = rng.standard_normal(256, dtype=np.float32)
     return [
         ("blk.0.ffn_gate.weight", (8, 512), 12, q4k),
         ("blk.0.ffn_down.weight", (4, 512), 14, q6k),
         ("blk.0.attn_q.weight", (3, 64), 8, q80),
+        ("blk.0.attn_k.weight", (2, 512), 11, q3k),
+        ("blk.0.attn_v.weight", (5, 96), 7, q51),
         ("output_norm.weight", (256,), 0, norm.tobytes()),
     ], norm
 
@@ -70,9 +74,11 @@ def test_roundtrip_metadata_and_directory(tmp_path):
         assert g.tensor("blk.0.ffn_down.weight").kernel_type == 14
         with pytest.raises(KeyError):
             g.tensor("nope")
-    with GGUFFile(path, q6k_layout="ggml") as g:
+    with GGUFFile(path, field_order="ggml") as g:
         assert g.tensor("blk.0.ffn_down.weight").kernel_type == 14 | Q6K_D_LAST
+        assert g.tensor("blk.0.attn_k.weight").kernel_type == 11 | Q6K_D_LAST
         assert g.tensor("blk.0.ffn_gate.weight").kernel_type == 12
+        assert g.tensor("blk.0.attn_v.weight").kernel_type == 7
 
 
 def test_custom_alignment(tmp_path):

@@ -41,7 +41,7 @@ def _file(tmp_path, q6k_ggml: bool):
 def test_upload_and_gemv(tmp_path, q6k_ggml):
     path, tensors, ref_w, norm, emb = _file(tmp_path, q6k_ggml)
     print(f"upload q6k_ggml={q6k_ggml}", flush=True)
-    with GGUFFile(path, q6k_layout="ggml" if q6k_ggml else "reference") as g:
+    with GGUFFile(path, field_order="ggml" if q6k_ggml else "reference") as g:
         up = upload_gguf(g, chunk_bytes=4096)
         for name, shape, ttype, payload in tensors:
             t = up[name]

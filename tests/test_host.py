@@ -14,6 +14,7 @@ import torch
 from dracort_amd import _native
 from dracort_amd.exceptions import DracoFormatError
 from dracort_amd.format import gguf as fmt
+from dracort_amd.quantization import quantize
 from oracle import gguf_ref
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -37,17 +38,23 @@ def test_library_exports_every_declared_symbol():
     assert lib.draco_gguf_abi_version() == _native.ABI_VERSION
 
 
-@pytest.mark.parametrize("qtype,expect", [(2, (32, 18)), (8, (32, 34)), (12, (256, 144)), (14, (256, 210)),
-                                          (14 | 0x100, (256, 210))])
+@pytest.mark.parametrize("qtype,expect", [
+    (2, (32, 18)), (3, (32, 20)), (6, (32, 22)), (7, (32, 24)), (8, (32, 34)), (15, (256, 258)),
+    (10, (256, 84)), (11, (256, 110)), (12, (256, 144)), (13, (256, 176)), (14, (256, 210)),
+    (10 | 0x100, (256, 84)), (11 | 0x100, (256, 110)), (14 | 0x100, (256, 210))])
 def test_block_info(qtype, expect):
     assert _native.block_info(qtype) == expect
     assert fmt.layout(qtype) == expect
 
 
 def test_block_info_rejects_unknown_types():
-    for bad in (0, 1, 3, 16, 8 | 0x100):
+    # F32 / F16 are not block types; 4, 5 were removed from ggml; 9 (Q8_1) and
+    # 16+ (IQ*) are not read by the reference; the order flag only fits Q2_K / Q3_K / Q6_K
+    for bad in (0, 1, 4, 5, 9, 16, 28, 8 | 0x100, 12 | 0x100, 13 | 0x100, 15 | 0x100):
         with pytest.raises(DracoFormatError):
             _native.block_info(bad)
+        with pytest.raises(DracoFormatError):
+            fmt.layout(bad)
 
 
 FAKE = 0x10000  # aligned, never dereferenced: every call below fails validation first
@@ -197,6 +204,40 @@ def test_gpu_tier_selection_rules():
     assert is_gguf_block_tensor(GgufTensorInfo("w", 12, (16, 256)))
     assert is_gguf_block_tensor(GgufTensorInfo("w", 14 | 0x100, (16, 256)))
     assert not is_gguf_block_tensor(GgufTensorInfo("w", 0, (16, 256)))          # float32
-    assert not is_gguf_block_tensor(GgufTensorInfo("w", 3, (16, 256)))          # Q4_1: no kernel here
+    assert is_gguf_block_tensor(GgufTensorInfo("w", 3, (16, 256)))              # Q4_1
+    assert is_gguf_block_tensor(GgufTensorInfo("w", 11 | 0x100, (16, 256)))     # Q3_K, ggml order
+    assert not is_gguf_block_tensor(GgufTensorInfo("w", 9, (16, 256)))          # Q8_1: not read by the reference
     assert not is_gguf_block_tensor(GgufTensorInfo("w", 12, (4096,)))           # not 2-D
     assert not is_gguf_block_tensor(GgufTensorInfo("w", 12, (16, 256), quantization="int8_sym"))
+
+
+def test_quantizers_match_reference_encoders_for_q4_1_q5_0_q5_1():
+    """The package's Q4_1 / Q5_0 / Q5_1 bytes are the reference test encoders'
+    (restated in oracle.encoders, tests/format/test_gguf.py:172-229)."""
+    from oracle import encoders
+
+    w = (np.random.default_rng(12).standard_normal((6, 256)) * 0.7).astype(np.float32)
+    w[2] = 0.0          # zero span: d = 1
+    w[3, :32] = 1.25    # constant block
+    for qtype, enc in ((3, encoders.enc_q4_1), (6, encoders.enc_q5_0), (7, encoders.enc_q5_1)):
+        got = quantize(torch.from_numpy(w), qtype).numpy()
+        assert np.array_equal(got, np.frombuffer(enc(w.reshape(-1)), np.uint8)), qtype
+
+
+@pytest.mark.parametrize("qtype", [10, 11, 14])
+def test_quantizer_ggml_order_is_the_field_move(qtype):
+    w = (np.random.default_rng(qtype).standard_normal((4, 512)) * 0.02).astype(np.float32)
+    ref = quantize(torch.from_numpy(w), qtype).numpy()
+    up = quantize(torch.from_numpy(w), qtype | 0x100).numpy()
+    assert np.array_equal(gguf_ref.to_ggml_order(qtype, ref), up)
+
+
+@pytest.mark.parametrize("qtype,tol", [(3, 0.08), (6, 0.06), (7, 0.04), (15, 0.01), (10, 0.45), (11, 0.25),
+                                       (13, 0.05)])
+def test_quantizers_round_trip(qtype, tol):
+    """Quantize -> oracle dequantize stays within each format's resolution (rms, relative)."""
+    w = (np.random.default_rng(qtype).standard_normal((16, 1024)) * 0.02).astype(np.float32)
+    b = quantize(torch.from_numpy(w), qtype).numpy()
+    deq = gguf_ref.dequantize_matrix(qtype, b, w.shape)
+    rms = np.sqrt(np.mean((deq - w) ** 2)) / np.sqrt(np.mean(w ** 2))
+    assert rms < tol, (qtype, rms)

@@ -50,7 +50,7 @@ def test_q6k_upstream_order_is_a_pure_field_move(golden):
     blocks = golden["Q6_K_blocks"]
     up = gguf_ref.q6k_reorder(blocks, to_upstream=True)
     assert not np.array_equal(up, blocks.reshape(-1))
-    got = gguf_ref.dequantize(14, up, blocks.shape[0] * 256, q6k_d_last=True)
+    got = gguf_ref.dequantize(14, up, blocks.shape[0] * 256, ggml_order=True)
     assert np.array_equal(got.view(np.uint32), golden["Q6_K_expect_bits"])
     assert np.array_equal(gguf_ref.q6k_reorder(up, to_upstream=False), blocks.reshape(-1))
 
@@ -232,7 +232,7 @@ def _dq_q6k_wrong_scale_index(b):
 
 
 def _dq_q6k_d_last_misread(b):
-    return gguf_ref.dequantize(14, b, b.shape[0] * 256, q6k_d_last=True)
+    return gguf_ref.dequantize(14, b, b.shape[0] * 256, ggml_order=True)
 
 
 @pytest.mark.parametrize(

@@ -247,6 +247,36 @@ def suite(reps: int):
     return lines
 
 
+def types_suite(reps: int):
+    """Decode GEMV of every GGUF block type at two Llama-3-8B shapes, M = 1
+    (bf16 and float32 activations) and M = 4, one JSON line each (stdout)."""
+    import torch
+
+    from dracort_amd.format.gguf import TYPE_NAMES, tensor_bytes
+    from dracort_amd.kernels import gguf_gemv
+    from dracort_amd.runtime.decode import synthetic_weight
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+    lines = []
+    for t in sorted(TYPE_NAMES):
+        for n, k in ((14336, 4096), (4096, 14336)):
+            nb = tensor_bytes(t, (n, k))
+            mats = rotation(lambda: synthetic_weight(n, k, t, gen, "cuda").data, nb)
+            for m, xdtype in ((1, torch.bfloat16), (1, torch.float32), (4, torch.bfloat16)):
+                x = torch.randn((m, k), device="cuda").to(xdtype)
+                y = torch.empty((m, n), device="cuda")
+                ms = time_launches([lambda w=w: gguf_gemv(x, w, t, (n, k), out=y) for w in mats], reps)
+                alg = nb + x.numel() * x.element_size() + y.numel() * 4
+                lines.append({"kernel": "decode GEMV", "ggml_type": TYPE_NAMES[t], "shape": [n, k], "m": m,
+                              "x_dtype": str(xdtype).replace("torch.", ""), "us_per_launch": round(ms * 1e3, 3),
+                              "GB_s": round(alg / (ms * 1e-3) / 1e9, 1),
+                              "frac_hbm_peak": round(alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "alg_bytes": alg})
+                log(json.dumps(lines[-1]))
+            del mats
+    return lines
+
+
 def traffic_probe(reps: int):
     """The roofline kernel's rotation plus a plain copy of known size, for the
     FETCH_SIZE / WRITE_SIZE counter runs (the copy calibrates the counters)."""
@@ -321,6 +351,7 @@ def main() -> int:
     ap.add_argument("--roofline-reps", type=int, default=20)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--suite", action="store_true", help="measure configurations 1, 2, 4, 5 (one JSON line each)")
+    ap.add_argument("--types", action="store_true", help="decode GEMV of every GGUF block type (one JSON line each)")
     ap.add_argument("--traffic-probe", action="store_true", help="run only the roofline rotation + a 256 MB copy")
     ap.add_argument("--mfma-probe", action="store_true", help="run only the configuration-4 GEMMs (counter runs)")
     ap.add_argument("--moe-probe", action="store_true", help="run only the configuration-5 MoE FFN (kernel traces)")
@@ -344,6 +375,10 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.suite:
         for line in suite(args.roofline_reps):
+            print(json.dumps(line), flush=True)
+        return 0
+    if args.types:
+        for line in types_suite(args.roofline_reps):
             print(json.dumps(line), flush=True)
         return 0
     if args.traffic_probe:

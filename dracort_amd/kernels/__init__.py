@@ -1,5 +1,12 @@
 """GPU operators of the GGUF quantized-matmul path (HIP kernels, gfx950)."""
 
+from dracort_amd.kernels.glue import (  # noqa: F401
+    DecodeAttentionWorkspace,
+    decode_attention,
+    decode_attention_workspace_bytes,
+    rms_norm,
+    rope_tables,
+)
 from dracort_amd.kernels.gguf import (  # noqa: F401
     block_layout,
     gemm_workspace_bytes,
@@ -26,4 +33,9 @@ __all__ = [
     "moe_workspace_bytes",
     "gemm_workspace_bytes",
     "block_layout",
+    "rms_norm",
+    "decode_attention",
+    "decode_attention_workspace_bytes",
+    "DecodeAttentionWorkspace",
+    "rope_tables",
 ]

@@ -189,6 +189,47 @@ int draco_gguf_moe_ffn(int ggml_type, const void* const* w_gate, const void* con
                        float* y, int64_t tokens, int64_t hidden, int64_t inter, int n_experts, int top_k,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * RMSNorm of m rows of n float32 values (n a multiple of 4):
+ *   y[r, i] = x[r, i] / sqrt(mean_j(x[r, j]^2) + eps) * weight[i]
+ * into float32 y and / or bfloat16 y_bf16 (either may be NULL, not both).
+ * Replaces rms_norm (draco/runtime/cpu/ops.py:15-19) as the executor's _norm
+ * (draco/runtime/cpu/executor.py:199-206) calls it.
+ */
+int draco_gguf_rms_norm(const float* x, const float* weight, float eps, float* y, void* y_bf16, int64_t m, int64_t n,
+                        void* stream);
+
+/*
+ * Workspace bytes draco_gguf_decode_attention needs (0 for invalid sizes).
+ * The workspace must be zeroed before its first use; the kernel leaves it
+ * ready for the next call.
+ */
+size_t draco_gguf_decode_attention_workspace_size(int64_t batch, int n_q_heads, int n_kv_heads, int head_dim,
+                                                  int64_t max_positions);
+
+/*
+ * One decode token per sequence b (batch sequences): rotate q [b, n_q_heads *
+ * head_dim] and k [b, n_kv_heads * head_dim] (float32) with RoPE at
+ * position p = positions[b] (device int32, 0 <= p < max_positions) using
+ * the tables rope_cos / rope_sin [max_positions][head_dim / 2] (float32, as
+ * build_rope_cache makes them, draco/runtime/cpu/ops.py:73-79; both NULL:
+ * no rotation), store k and v in the float16 caches
+ * k_cache / v_cache [batch][n_kv_heads][max_positions][head_dim] at that
+ * position, and write the attention of q over positions 0 .. p of its
+ * sequence (query head h reads kv head h / (n_q_heads / n_kv_heads);
+ * scores q.k / sqrt(head_dim), softmax, weighted sum of v) to out
+ * [b, n_q_heads * head_dim], float32 or bfloat16 (out_dtype).  head_dim 64
+ * or 128, up to 8 query heads per kv head.  A position outside
+ * [0, max_positions) touches no cache memory and yields NaN outputs.
+ * Replaces apply_rope (draco/runtime/cpu/ops.py:73-92) on q / k and
+ * CPUAttentionBackend.decode (draco/runtime/cpu/attention.py:35-81) with its
+ * CPUKVCache append (float16 storage, draco/runtime/cpu/kv_cache.py:19-28).
+ */
+int draco_gguf_decode_attention(const float* q, const float* k, const float* v, void* k_cache, void* v_cache,
+                                const int32_t* positions, int64_t batch, int n_q_heads, int n_kv_heads, int head_dim,
+                                int64_t max_positions, const float* rope_cos, const float* rope_sin, void* out,
+                                int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

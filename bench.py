@@ -173,6 +173,37 @@ def cpu_baseline(ls, step_bytes):
     }
 
 
+def full_decode(ls, batch: int, context: int, steps: int, warmup: int):
+    """The full decode step (RMSNorms, RoPE + KV-cache attention, projections,
+    lm_head) on the same layer set, ``context`` tokens already cached per
+    sequence, one HIP graph per step; positions advance every step."""
+    import torch
+
+    from dracort_amd.runtime.decode import AttentionShape, DecodeStep
+
+    attn = AttentionShape(max_positions=context + warmup + steps + 2)
+    step = DecodeStep(ls, m=batch, attention=attn, start_position=context)
+    step.capture()
+    for _ in range(warmup):
+        step.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        step.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    kv_bytes = 2 * len(ls.layers) * batch * attn.n_kv_heads * attn.head_dim * 2 * (context + warmup + steps // 2)
+    out = {"batch": batch, "context": context, "ms_per_step": round(ms, 4),
+           "tokens_per_s": round(batch * 1e3 / ms, 2), "kv_cache_bytes_read_per_step": kv_bytes,
+           "note": "per layer: RMSNorm, q/k/v, RoPE + float16 KV append + GQA attention, o + residual, RMSNorm, "
+                   "gate/up SwiGLU, down + residual; final RMSNorm, lm_head"}
+    del step
+    torch.cuda.empty_cache()
+    return out
+
+
 def rotation(make, nbytes, min_total=1 << 30):
     """Distinct copies of a synthetic weight so that a timed rotation streams
     >= min_total bytes (beyond the 256 MB Infinity Cache)."""
@@ -218,6 +249,17 @@ def suite(reps: int):
     for t, n, k in ((12, 14336, 4096), (12, 4096, 4096), (14, 4096, 14336), (14, 128256, 4096)):
         for m in (1, 16):
             lines.append(gemv_line(3, t, n, k, m, torch.bfloat16))
+    # 3 (full step): norms + RoPE / KV-cache attention + projections, contexts 1024 / 4096, batch 1 / 16
+    from dracort_amd.runtime.decode import LlamaShape, synthetic_layer_set
+
+    ls = synthetic_layer_set(LlamaShape(n_layers=32), seed=0, device="cuda")
+    for batch, context in ((1, 1024), (1, 4096), (16, 1024)):
+        d = full_decode(ls, batch, context, 20, 2)
+        d.update({"config": 3, "kernel": "full decode step (HIP graph)"})
+        lines.append(d)
+        log(json.dumps(d))
+    del ls
+    torch.cuda.empty_cache()
     # 4: prefill GEMM, Q4_K weights, bf16 activations, M = 512 / 2048
     for n, k in ((14336, 4096), (4096, 14336)):
         w = synthetic_weight(n, k, 12, gen, "cuda")
@@ -350,6 +392,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--roofline-reps", type=int, default=20)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--full-context", type=int, default=1024,
+                    help="also time the full decode step (norms + attention) at this context (0: skip)")
     ap.add_argument("--suite", action="store_true", help="measure configurations 1, 2, 4, 5 (one JSON line each)")
     ap.add_argument("--types", action="store_true", help="decode GEMV of every GGUF block type (one JSON line each)")
     ap.add_argument("--traffic-probe", action="store_true", help="run only the roofline rotation + a 256 MB copy")
@@ -421,6 +465,11 @@ def main() -> int:
     log(f"decode step: {ms:.3f} ms (wall {wall / args.steps * 1e3:.3f} ms), {gbs:.1f} GB/s, "
         f"{args.batch * 1e3 / ms:.1f} tokens/s")
 
+    full = None
+    if args.full_context > 0:
+        full = full_decode(ls, args.batch, args.full_context, max(10, args.steps // 2), 2)
+        log(f"full decode step: {full}")
+
     roof = dominant_kernel_roofline(ls, args.roofline_reps)
     log(f"roofline: {roof}")
 
@@ -458,6 +507,7 @@ def main() -> int:
         },
         "tokens_per_s": round(args.batch * 1e3 / ms, 2),
         "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "full_decode": full,
         "roofline": roof,
         "cpu_baseline": cpu,
     }

@@ -20,9 +20,10 @@
 //   * the new token's k / v are rotated, rounded to float16 and used directly
 //     by the workgroup whose range holds their position, which also stores
 //     them in the cache (no other workgroup reads that position);
-//   * the last workgroup of a (sequence, kv head) to finish -- found with a
-//     device-scope counter, no waiting -- merges the partial states and writes
-//     the output; it resets the counter, so the workspace needs zeroing once.
+//   * only the workgroups whose range holds keys (positions 0 .. p) do any
+//     work; a second launch, one workgroup per (sequence, kv head), merges
+//     their partial states (max over the splits, rescaled sums) and writes the
+//     output.
 #include <math.h>
 
 #include "draco_internal.h"
@@ -39,25 +40,42 @@ __device__ __forceinline__ float block_sum_256(float v, float* red) {
   return red[0] + red[1] + red[2] + red[3];
 }
 
+// Max over the 64 lanes, result in every lane (DPP within rows of 16, then two exchanges).
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
+// Sum over aligned groups of N (8 or 16) lanes, result in every lane of the group.
+template <int N>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  if constexpr (N == 16) v += dpp_f<0x140>(v);
+  return v;
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);
   u += 0x7FFFu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
 }
 
+// One row per workgroup.  NV > 0: the row (n <= 1024 NV) is loaded in one
+// batch into registers (every load in flight at once); NV = 0: any n, in a loop.
+template <int NV>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                        float eps, float* __restrict__ y, uint16_t* __restrict__ yb,
                                                        int n) {
   __shared__ float red[4];
   const float* xr = x + (size_t)blockIdx.x * n;
-  float ss = 0.f;
-  for (int i = threadIdx.x * 4; i < n; i += 1024) {
-    const float4 v = *reinterpret_cast<const float4*>(xr + i);
-    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-  }
-  const float denom = sqrtf(block_sum_256(ss, red) / (float)n + eps);
-  for (int i = threadIdx.x * 4; i < n; i += 1024) {
-    const float4 v = *reinterpret_cast<const float4*>(xr + i);
+  auto emit = [&](int i, float4 v, float denom) {
     const float4 g = *reinterpret_cast<const float4*>(w + i);
     const float4 o = make_float4(v.x / denom * g.x, v.y / denom * g.y, v.z / denom * g.z, v.w / denom * g.w);
     const size_t at = (size_t)blockIdx.x * n + i;
@@ -67,12 +85,42 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
       const uint32_t hi = f32_to_bf16_bits(o.z) | ((uint32_t)f32_to_bf16_bits(o.w) << 16);
       *reinterpret_cast<uint2*>(yb + at) = make_uint2(lo, hi);
     }
+  };
+  if constexpr (NV > 0) {
+    float4 v[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int r = 0; r < NV; ++r) {
+      const int i = threadIdx.x * 4 + 1024 * r;
+      v[r] = i < n ? *reinterpret_cast<const float4*>(xr + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int r = 0; r < NV; ++r) ss += v[r].x * v[r].x + v[r].y * v[r].y + v[r].z * v[r].z + v[r].w * v[r].w;
+    const float denom = sqrtf(block_sum_256(ss, red) / (float)n + eps);
+#pragma unroll
+    for (int r = 0; r < NV; ++r) {
+      const int i = threadIdx.x * 4 + 1024 * r;
+      if (i < n) emit(i, v[r], denom);
+    }
+  } else {
+    float ss = 0.f;
+    for (int i = threadIdx.x * 4; i < n; i += 1024) {
+      const float4 v = *reinterpret_cast<const float4*>(xr + i);
+      ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    const float denom = sqrtf(block_sum_256(ss, red) / (float)n + eps);
+    for (int i = threadIdx.x * 4; i < n; i += 1024) emit(i, *reinterpret_cast<const float4*>(xr + i), denom);
   }
 }
 
 int rms_norm_launch(const float* x, const float* w, float eps, float* y, uint16_t* yb, int64_t m, int64_t n,
                     hipStream_t s) {
-  hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)m), dim3(256), 0, s, x, w, eps, y, yb, (int)n);
+  if (n <= 4096)
+    hipLaunchKernelGGL(rms_norm_kernel<4>, dim3((unsigned)m), dim3(256), 0, s, x, w, eps, y, yb, (int)n);
+  else if (n <= 16384)
+    hipLaunchKernelGGL(rms_norm_kernel<16>, dim3((unsigned)m), dim3(256), 0, s, x, w, eps, y, yb, (int)n);
+  else
+    hipLaunchKernelGGL(rms_norm_kernel<0>, dim3((unsigned)m), dim3(256), 0, s, x, w, eps, y, yb, (int)n);
   return check_launch("rms_norm");
 }
 
@@ -80,7 +128,8 @@ int rms_norm_launch(const float* x, const float* w, float eps, float* y, uint16_
 // decode attention
 // ---------------------------------------------------------------------------
 constexpr int kAttnChunk = 256;  // positions per workgroup
-constexpr int kMaxGroup = 8;     // query heads per kv head
+constexpr int kMaxSplits = 512;  // splits per (sequence, kv head): max_positions <= 131072
+constexpr int kMaxGroup = 8;     // query heads per kv head (1, 2, 4 or 8)
 
 struct AttnArgs {
   const float* q;          // [B, Hq * D]
@@ -90,8 +139,7 @@ struct AttnArgs {
   uint16_t* vc;
   const int* positions;    // [B]
   void* out;               // [B, Hq * D] float32 or bfloat16
-  float* part;             // [B, Hkv, S, G, D + 2]
-  unsigned* count;         // [B, Hkv]
+  float* part;             // [B, Hkv, S, G, D + 2] partial softmax states
   const float* cos_t;      // [P, D / 2] RoPE tables, NULL: no rotation
   const float* sin_t;
   int hq, hkv, max_pos, splits;
@@ -111,30 +159,44 @@ __device__ __forceinline__ void rope_pair(const AttnArgs& a, int pos, int i, int
   x2 = r2;
 }
 
-template <int D>
+template <int D, int G>
 __global__ __launch_bounds__(256) void decode_attention_kernel(AttnArgs a) {
   constexpr int HALF = D / 2;
-  __shared__ float qs[kMaxGroup][D];     // rotated queries of the group
-  __shared__ float kn[D];                // the new token's rotated key (float16-rounded)
+  constexpr int LK = D / 8;            // lanes per key: each holds 8 dimensions (one 16-byte load)
+  constexpr int KS = 256 / LK;         // keys per pass of the workgroup
+  constexpr int NP = kAttnChunk / KS;  // passes over the chunk
+  constexpr bool EARLY_V = G <= 4;     // value loads issued with the key loads (register budget)
+  __shared__ float qs[G][D];           // rotated queries of the group
+  __shared__ float kn[D];              // the new token's rotated key (float16-rounded)
   __shared__ float vn[D];
-  __shared__ float ps[kMaxGroup][kAttnChunk];
-  __shared__ float red[kMaxGroup][4];
-  constexpr int SETS = 256 / D;  // thread sets splitting the keys of the value sums
-  __shared__ float accs[SETS - 1][kMaxGroup][D];
-  __shared__ int last;
+  __shared__ float ps[G][kAttnChunk];
+  __shared__ float red[G][4];
+  __shared__ float accs[KS][D];        // one query head's value sums per key slot
 
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int G = a.hq / a.hkv;
   const int t = threadIdx.x;
   const int pos = a.positions[b];
   const bool valid = pos >= 0 && pos < a.max_pos;  // else no cache access; the output is NaN
   const int n_keys = valid ? pos + 1 : 0;
+  const int used = (n_keys + kAttnChunk - 1) / kAttnChunk;  // workgroups holding keys
   const int j0 = split * kAttnChunk;
   const int jn = min(kAttnChunk, n_keys - j0);  // keys of this workgroup (<= 0: none)
+  if (split >= used || jn <= 0) return;  // no keys
   const size_t head = ((size_t)b * a.hkv + h) * (size_t)a.max_pos * D;
   float* part = a.part + (((size_t)b * a.hkv + h) * a.splits + split) * G * (D + 2);
+  // thread t: dimensions 8 * (t % LK) .. + 7 of key slot t / LK of each pass
+  const int dl = t % LK, slot = t / LK;
 
   if (jn > 0) {
+    // every key (and value) load of the chunk first: their addresses need only the position
+    uint4 kw[NP], vw[EARLY_V ? NP : 1];
+#pragma unroll
+    for (int r = 0; r < NP; ++r) {
+      const int jj = slot + KS * r;
+      const size_t at = head + (size_t)(j0 + (jj < jn ? jj : 0)) * D + 8 * dl;
+      kw[r] = *reinterpret_cast<const uint4*>(a.kc + at);
+      if constexpr (EARLY_V) vw[r] = *reinterpret_cast<const uint4*>(a.vc + at);
+    }
     // queries (and, for the workgroup holding the new position, k / v), rotated
     for (int e = t; e < G * HALF; e += 256) {
       const int g = e / HALF, i = e - g * HALF;
@@ -165,151 +227,173 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // scores: thread t <-> key j0 + t
-    float sc[kMaxGroup];
+    float qr[G][8];
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) sc[g] = -INFINITY;
-    if (t < jn) {
-      const int j = j0 + t;
-      float dot[kMaxGroup];
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int g = 0; g < kMaxGroup; ++g) dot[g] = 0.f;
-      if (j == pos) {
-        for (int i = 0; i < D; ++i) {
-#pragma unroll
-          for (int g = 0; g < kMaxGroup; ++g)
-            if (g < G) dot[g] = fmaf(qs[g][i], kn[i], dot[g]);
-        }
-      } else {
-        const uint4* kp = reinterpret_cast<const uint4*>(a.kc + head + (size_t)j * D);
-        for (int c = 0; c < D / 8; ++c) {
-          const uint4 w = kp[c];
-          const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float k0 = f16_to_f32((uint16_t)(ws[e] & 0xFFFFu)), k1 = f16_to_f32((uint16_t)(ws[e] >> 16));
-            const int i = 8 * c + 2 * e;
-#pragma unroll
-            for (int g = 0; g < kMaxGroup; ++g)
-              if (g < G) dot[g] = fmaf(qs[g][i + 1], k1, fmaf(qs[g][i], k0, dot[g]));
-          }
-        }
-      }
-#pragma unroll
-      for (int g = 0; g < kMaxGroup; ++g) sc[g] = dot[g] * a.scale;
-    }
-    // max and sum of exponentials per query head
-    float m[kMaxGroup], l[kMaxGroup];
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) {
-      if (g >= G) break;
-      float v = sc[g];
-      v = fmaxf(v, __shfl_xor(v, 1, 64));
-      v = fmaxf(v, __shfl_xor(v, 2, 64));
-      v = fmaxf(v, __shfl_xor(v, 4, 64));
-      v = fmaxf(v, __shfl_xor(v, 8, 64));
-      v = fmaxf(v, __shfl_xor(v, 16, 64));
-      v = fmaxf(v, __shfl_xor(v, 32, 64));
-      if ((t & 63) == 0) red[g][t >> 6] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) {
-      if (g >= G) break;
-      m[g] = fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3]));
-      const float p = t < jn ? expf(sc[g] - m[g]) : 0.f;
-      ps[g][t] = p;
-      sc[g] = p;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) {
-      if (g >= G) break;
-      float v = wave_sum_dpp(sc[g]);
-      if ((t & 63) == 0) red[g][t >> 6] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) {
-      if (g >= G) break;
-      l[g] = red[g][0] + red[g][1] + red[g][2] + red[g][3];
-    }
-    // weighted value sums: thread t <-> dimension t % D, keys split over the thread sets
-    const int d = t % D, set = t / D;
-    float o[kMaxGroup];
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) o[g] = 0.f;
-    for (int jj = set; jj < jn; jj += SETS) {
-      const int j = j0 + jj;
-      const float vv = j == pos ? vn[d] : f16_to_f32(a.vc[head + (size_t)j * D + d]);
-#pragma unroll
-      for (int g = 0; g < kMaxGroup; ++g)
-        if (g < G) o[g] = fmaf(ps[g][jj], vv, o[g]);
-    }
-    if (set > 0) {
-#pragma unroll
-      for (int g = 0; g < kMaxGroup; ++g)
-        if (g < G) accs[set - 1][g][d] = o[g];
-    }
-    __syncthreads();
-    if (set == 0) {
-      for (int r = 0; r < SETS - 1; ++r) {
-#pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g)
-          if (g < G) o[g] += accs[r][g][d];
-      }
-    }
-    if (set == 0) {
-#pragma unroll
-      for (int g = 0; g < kMaxGroup; ++g) {
-        if (g >= G) break;
-        part[g * (D + 2) + 2 + d] = o[g];
-        if (d == 0) {
-          part[g * (D + 2)] = m[g];
-          part[g * (D + 2) + 1] = l[g];
-        }
-      }
-    }
-  }
+      for (int e = 0; e < 8; ++e) qr[g][e] = qs[g][8 * dl + e];
 
-  // the last workgroup of (b, h) merges the partial states
-  __threadfence();
-  __syncthreads();
-  if (t == 0) {
-    const unsigned done = atomicAdd(a.count + (size_t)b * a.hkv + h, 1u);
-    last = done == (unsigned)a.splits - 1;
+    // scores (the new position's key comes from LDS)
+#pragma unroll
+    for (int r = 0; r < NP; ++r) {
+      const int jj = slot + KS * r;
+      float kv[8];
+      if (j0 + jj == pos) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kv[e] = kn[8 * dl + e];
+      } else {
+        const uint32_t ws[4] = {kw[r].x, kw[r].y, kw[r].z, kw[r].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          kv[2 * e] = f16_to_f32((uint16_t)(ws[e] & 0xFFFFu));
+          kv[2 * e + 1] = f16_to_f32((uint16_t)(ws[e] >> 16));
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dot = fmaf(qr[g][e], kv[e], dot);
+        dot = group_sum_dpp<LK>(dot);  // the key's LK lanes
+        if (dl == 0) ps[g][jj] = jj < jn ? dot * a.scale : -INFINITY;
+      }
+    }
+    if constexpr (!EARLY_V) {
+#pragma unroll
+      for (int r = 0; r < NP; ++r) {
+        const int jj = slot + KS * r;
+        kw[r] = *reinterpret_cast<const uint4*>(a.vc + head + (size_t)(j0 + (jj < jn ? jj : 0)) * D + 8 * dl);
+      }
+    }
+    __syncthreads();
+
+    // max and sum of exponentials per query head (thread t < chunk <-> key t)
+    float m[G], l[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float v = wave_max_dpp(t < kAttnChunk ? ps[g][t] : -INFINITY);
+      if ((t & 63) == 0) red[g][t >> 6] = v;
+    }
+    __syncthreads();
+    float pv[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3]));
+      pv[g] = t < jn ? expf(ps[g][t] - m[g]) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (t < kAttnChunk) ps[g][t] = pv[g];
+      const float v = wave_sum_dpp(pv[g]);
+      if ((t & 63) == 0) red[g][t >> 6] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) l[g] = red[g][0] + red[g][1] + red[g][2] + red[g][3];
+
+    // weighted value sums, the same lane mapping
+    float o[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
+#pragma unroll
+    for (int r = 0; r < NP; ++r) {
+      const int jj = slot + KS * r;
+      const uint4 w = EARLY_V ? vw[EARLY_V ? r : 0] : kw[r];
+      float vv[8];
+      if (j0 + jj == pos) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vv[e] = vn[8 * dl + e];
+      } else {
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vv[2 * e] = f16_to_f32((uint16_t)(ws[e] & 0xFFFFu));
+          vv[2 * e + 1] = f16_to_f32((uint16_t)(ws[e] >> 16));
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float p = jj < jn ? ps[g][jj] : 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] = fmaf(p, vv[e], o[g][e]);
+      }
+    }
+    // sum over the KS key slots through LDS, one query head at a time
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) accs[slot][8 * dl + e] = o[g][e];
+      __syncthreads();
+      if (t < D) {
+        float v = 0.f;
+#pragma unroll
+        for (int k2 = 0; k2 < KS; ++k2) v += accs[k2][t];
+        part[g * (D + 2) + 2 + t] = v;
+      }
+      __syncthreads();
+    }
+    if (t < G) {
+      part[t * (D + 2)] = m[t];
+      part[t * (D + 2) + 1] = l[t];
+    }
+  }
+}
+
+// Merges the partial states of the `used` workgroups of (sequence b, kv head h)
+// (a second launch: the kernel boundary makes the partials visible).
+template <int D, int G>
+__global__ __launch_bounds__(256) void decode_merge_kernel(AttnArgs a) {
+  __shared__ float ms[kMaxSplits][G];  // split maxima, then their weights exp(m_s - M)
+  __shared__ float ls[kMaxSplits][G];
+  __shared__ float mg[G], dg[G];
+  const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int pos = a.positions[b];
+  const bool valid = pos >= 0 && pos < a.max_pos;
+  const int used = valid ? (pos + kAttnChunk) / kAttnChunk : 0;
+  const float* base = a.part + ((size_t)b * a.hkv + h) * a.splits * G * (D + 2);
+  for (int i = t; i < used * G; i += 256) {
+    const int sp = i / G, g = i - sp * G;
+    ms[sp][g] = base[(sp * G + g) * (D + 2)];
+    ls[sp][g] = base[(sp * G + g) * (D + 2) + 1];
   }
   __syncthreads();
-  if (!last) return;
-  __threadfence();
-  const int used = (n_keys + kAttnChunk - 1) / kAttnChunk;  // splits that hold keys
-  const float* base = a.part + ((size_t)b * a.hkv + h) * a.splits * G * (D + 2);
+  if (t < G) {
+    float mx = -INFINITY;
+    for (int sp = 0; sp < used; ++sp) mx = fmaxf(mx, ms[sp][t]);
+    mg[t] = mx;
+  }
+  __syncthreads();
+  for (int i = t; i < used * G; i += 256) {
+    const int sp = i / G, g = i - sp * G;
+    ms[sp][g] = expf(ms[sp][g] - mg[g]);
+  }
+  __syncthreads();
+  if (t < G) {
+    float den = 0.f;
+    for (int sp = 0; sp < used; ++sp) den = fmaf(ls[sp][t], ms[sp][t], den);
+    dg[t] = den;
+  }
+  __syncthreads();
   for (int e = t; e < G * D; e += 256) {
     const int g = e / D, d = e - g * D;
-    float mx = -INFINITY;
-    for (int s = 0; s < used; ++s) mx = fmaxf(mx, base[(s * G + g) * (D + 2)]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < used; ++s) {
-      const float* p = base + (s * G + g) * (D + 2);
-      const float f = expf(p[0] - mx);
-      den = fmaf(p[1], f, den);
-      num = fmaf(p[2 + d], f, num);
-    }
-    const float r = valid ? num / den : __builtin_nanf("");
+    float num = 0.f;
+#pragma unroll 8
+    for (int sp = 0; sp < used; ++sp) num = fmaf(base[(sp * G + g) * (D + 2) + 2 + d], ms[sp][g], num);
+    const float r = valid ? num / dg[g] : __builtin_nanf("");
     const size_t at = (size_t)b * a.hq * D + (size_t)(h * G + g) * D + d;
     if (a.out_bf16)
       static_cast<uint16_t*>(a.out)[at] = f32_to_bf16_bits(r);
     else
       static_cast<float*>(a.out)[at] = r;
   }
-  if (t == 0) atomicExch(a.count + (size_t)b * a.hkv + h, 0u);
 }
 
 size_t decode_attention_ws(int64_t batch, int hq, int hkv, int head_dim, int64_t max_pos) {
   const int64_t splits = (max_pos + kAttnChunk - 1) / kAttnChunk;
-  const size_t part = (size_t)batch * hkv * splits * (hq / hkv) * (head_dim + 2) * sizeof(float);
-  const size_t count = (size_t)batch * hkv * sizeof(unsigned);
-  return ((count + 255) & ~(size_t)255) + part;
+  return (size_t)batch * hkv * splits * (hq / hkv) * (head_dim + 2) * sizeof(float);
 }
 
 int decode_attention_launch(const float* q, const float* k, const float* v, uint16_t* kc, uint16_t* vc,
@@ -324,9 +408,7 @@ int decode_attention_launch(const float* q, const float* k, const float* v, uint
   a.vc = vc;
   a.positions = positions;
   a.out = out;
-  a.count = static_cast<unsigned*>(workspace);
-  const size_t count = (size_t)batch * hkv * sizeof(unsigned);
-  a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((count + 255) & ~(size_t)255));
+  a.part = static_cast<float*>(workspace);
   a.hq = hq;
   a.hkv = hkv;
   a.max_pos = (int)max_pos;
@@ -336,11 +418,31 @@ int decode_attention_launch(const float* q, const float* k, const float* v, uint
   a.scale = (float)(1.0 / sqrt((double)head_dim));
   a.out_bf16 = out_bf16;
   const dim3 grid((unsigned)a.splits, (unsigned)hkv, (unsigned)batch);
-  if (head_dim == 128)
-    hipLaunchKernelGGL(decode_attention_kernel<128>, grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL(decode_attention_kernel<64>, grid, dim3(256), 0, s, a);
-  return check_launch("decode_attention");
+  const int g = hq / hkv;
+  const dim3 mgrid((unsigned)hkv, (unsigned)batch);
+#define DRACO_ATTN_LAUNCH(D_, G_)                                                                \
+  hipLaunchKernelGGL((decode_attention_kernel<D_, G_>), grid, dim3(256), 0, s, a);              \
+  if (int rc = check_launch("decode_attention")) return rc;                                    \
+  hipLaunchKernelGGL((decode_merge_kernel<D_, G_>), mgrid, dim3(256), 0, s, a)
+  if (head_dim == 128) {
+    switch (g) {
+      case 1: DRACO_ATTN_LAUNCH(128, 1); break;
+      case 2: DRACO_ATTN_LAUNCH(128, 2); break;
+      case 4: DRACO_ATTN_LAUNCH(128, 4); break;
+      case 8: DRACO_ATTN_LAUNCH(128, 8); break;
+      default: return set_error(DRACO_EINVAL_SHAPE, "query heads per kv head must be 1, 2, 4 or 8, got %d", g);
+    }
+  } else {
+    switch (g) {
+      case 1: DRACO_ATTN_LAUNCH(64, 1); break;
+      case 2: DRACO_ATTN_LAUNCH(64, 2); break;
+      case 4: DRACO_ATTN_LAUNCH(64, 4); break;
+      case 8: DRACO_ATTN_LAUNCH(64, 8); break;
+      default: return set_error(DRACO_EINVAL_SHAPE, "query heads per kv head must be 1, 2, 4 or 8, got %d", g);
+    }
+  }
+#undef DRACO_ATTN_LAUNCH
+  return check_launch("decode_attention_merge");
 }
 
 }  // namespace draco
@@ -376,15 +478,16 @@ int draco_gguf_decode_attention(const float* q, const float* k, const float* v, 
                                 int64_t max_positions, const float* rope_cos, const float* rope_sin, void* out,
                                 int out_dtype, void* workspace, size_t workspace_bytes, void* stream) {
   if (batch < 1 || batch > 65535 || n_kv_heads < 1 || n_kv_heads > 65535 || n_q_heads < n_kv_heads ||
-      n_q_heads % n_kv_heads || n_q_heads / n_kv_heads > kMaxGroup)
+      n_q_heads % n_kv_heads || n_q_heads / n_kv_heads > kMaxGroup ||
+      ((n_q_heads / n_kv_heads) & (n_q_heads / n_kv_heads - 1)))
     return set_error(DRACO_EINVAL_SHAPE,
-                     "decode attention needs 1 <= batch <= 65535, n_q_heads a multiple (<= %d x) of n_kv_heads; got "
+                     "decode attention needs 1 <= batch <= 65535, n_q_heads = 1, 2, 4 or 8 (<= %d) x n_kv_heads; got "
                      "batch %lld, %d / %d heads",
                      kMaxGroup, (long long)batch, n_q_heads, n_kv_heads);
   if (head_dim != 64 && head_dim != 128)
     return set_error(DRACO_EINVAL_SHAPE, "decode attention takes head_dim 64 or 128, got %d", head_dim);
   if (max_positions < 1 || max_positions * head_dim * (int64_t)n_kv_heads * batch > ((int64_t)1 << 40) ||
-      max_positions > (1 << 24))
+      max_positions > (int64_t)kMaxSplits * kAttnChunk)
     return set_error(DRACO_EINVAL_SHAPE, "invalid max_positions %lld", (long long)max_positions);
   if ((rope_cos == nullptr) != (rope_sin == nullptr))
     return set_error(DRACO_EINVAL_ARG, "rope_cos and rope_sin must both be given or both be NULL");

@@ -65,15 +65,15 @@ def decode_attention_workspace_bytes(batch: int, n_q_heads: int, n_kv_heads: int
 
 
 class DecodeAttentionWorkspace:
-    """Zero-initialised device workspace of the decode attention (its merge
-    counters must start at zero; every call leaves them at zero)."""
+    """Device workspace of the decode attention: the partial softmax states
+    of its position splits (reused by every call of the same sizes)."""
 
     def __init__(self, batch: int, n_q_heads: int, n_kv_heads: int, head_dim: int, max_positions: int,
                  device="cuda") -> None:
         nbytes = decode_attention_workspace_bytes(batch, n_q_heads, n_kv_heads, head_dim, max_positions)
         if nbytes == 0:
             raise ValueError("invalid decode attention sizes")
-        self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        self.buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
         self.sizes = (batch, n_q_heads, n_kv_heads, head_dim, max_positions)
 
 

@@ -11,9 +11,17 @@ the whole step can be captured into one HIP graph.  The projection inputs are
 bfloat16 (each launch writes the bf16 copy its consumer reads); the residual
 stream and the logits are float32.
 
-Only the projections are modelled: attention over the KV cache and the RMS
-norms are out of this path (the attention output fed to ``o_proj`` is the q
-projection itself), so a step streams exactly the layer set's weight bytes.
+Two forms of the step:
+
+* projections only (``attention=None``): the attention output fed to
+  ``o_proj`` is the q projection itself and there are no norms, so a step
+  streams exactly the layer set's weight bytes (the headline workload);
+* the full decode step (``attention=AttentionShape(...)``): per layer
+  RMSNorm -> q/k/v -> RoPE + KV-cache append + attention -> o_proj (+ residual)
+  -> RMSNorm -> gate/up SwiGLU -> down (+ residual), then the final RMSNorm and
+  the lm_head, as ``forward_step`` runs it
+  (``draco/runtime/cpu/executor.py:290-342``); every step appends one token
+  per sequence to the float16 caches and advances the device positions.
 """
 
 from __future__ import annotations
@@ -24,6 +32,7 @@ from typing import Dict, List, Optional
 import torch
 
 from dracort_amd.format.gguf import GGML_TYPE_Q4_K, GGML_TYPE_Q6_K, tensor_bytes
+from dracort_amd.kernels.glue import DecodeAttentionWorkspace, decode_attention, rms_norm, rope_tables
 from dracort_amd.kernels.gguf import gguf_gemv, gguf_gemv_multi, gguf_gemv_residual, gguf_gemv_swiglu
 from dracort_amd.quantization.gguf import GGUFQuantizedWeight
 from dracort_amd.quantization.quantize import quantize
@@ -52,10 +61,25 @@ Q4_K_M_TYPES = {"q": GGML_TYPE_Q4_K, "k": GGML_TYPE_Q4_K, "v": GGML_TYPE_Q4_K, "
 
 
 @dataclass
+class AttentionShape:
+    """Llama-3-8B attention: 32 query heads, 8 kv heads of 128, RoPE theta 500000."""
+
+    n_heads: int = 32
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    rope_theta: float = 500000.0
+    rms_eps: float = 1e-5
+    max_positions: int = 8192
+
+
+@dataclass
 class LayerSet:
     shape: LlamaShape
     layers: List[Dict[str, GGUFQuantizedWeight]] = field(default_factory=list)
     lm_head: Optional[GGUFQuantizedWeight] = None
+    # float32 RMSNorm weights per layer ("attn", "ffn") and the final one
+    norms: List[Dict[str, torch.Tensor]] = field(default_factory=list)
+    output_norm: Optional[torch.Tensor] = None
 
     @property
     def weight_bytes(self) -> int:
@@ -86,6 +110,10 @@ def synthetic_layer_set(shape: LlamaShape, seed: int = 0, device="cuda", types=N
             layer[name] = synthetic_weight(n, k, types[name], gen, device)
         ls.layers.append(layer)
     ls.lm_head = synthetic_weight(shape.vocab, shape.hidden, lm_head_type, gen, device)
+    for _ in range(shape.n_layers):
+        ls.norms.append({p: 1.0 + 0.1 * torch.randn(shape.hidden, generator=gen, device=device)
+                         for p in ("attn", "ffn")})
+    ls.output_norm = 1.0 + 0.1 * torch.randn(shape.hidden, generator=gen, device=device)
     return ls
 
 
@@ -96,11 +124,14 @@ def layer_set_bytes(shape: LlamaShape, types=None, lm_head_type: int = GGML_TYPE
 
 
 class DecodeStep:
-    """Preallocated buffers + the projection chain for a batch of `m` tokens."""
+    """Preallocated buffers + the decode chain for a batch of `m` tokens (one
+    per sequence); ``attention`` selects the full step (see the module doc),
+    with ``start_position`` tokens already cached per sequence."""
 
-    def __init__(self, ls: LayerSet, m: int = 1, device="cuda") -> None:
+    def __init__(self, ls: LayerSet, m: int = 1, device="cuda", attention: Optional[AttentionShape] = None,
+                 start_position: int = 0) -> None:
         s = ls.shape
-        self.ls, self.m = ls, m
+        self.ls, self.m, self.attn = ls, m, attention
         f32 = dict(dtype=torch.float32, device=device)
         b16 = dict(dtype=torch.bfloat16, device=device)
         gen = torch.Generator(device=device).manual_seed(1234)
@@ -113,8 +144,29 @@ class DecodeStep:
         self.s = torch.empty((m, s.inter), **b16)
         self.logits = torch.empty((m, s.vocab), **f32)
         self.graph: Optional[torch.cuda.CUDAGraph] = None
+        if attention is not None:
+            a = attention
+            if a.n_heads * a.head_dim != s.hidden or a.n_kv_heads * a.head_dim != s.kv_dim:
+                raise ValueError("attention heads do not match the projection shapes")
+            if not ls.norms or ls.output_norm is None:
+                raise ValueError("the full decode step needs the layer set's RMSNorm weights")
+            if not 0 <= start_position < a.max_positions:
+                raise ValueError(f"start_position must be in [0, {a.max_positions})")
+            cache = (m, a.n_kv_heads, a.max_positions, a.head_dim)
+            self.k_cache = [torch.zeros(cache, dtype=torch.float16, device=device) for _ in ls.layers]
+            self.v_cache = [torch.zeros(cache, dtype=torch.float16, device=device) for _ in ls.layers]
+            self.positions = torch.full((m,), start_position, dtype=torch.int32, device=device)
+            self.rope = rope_tables(a.head_dim, a.max_positions, a.rope_theta, device)
+            self.ws = DecodeAttentionWorkspace(m, a.n_heads, a.n_kv_heads, a.head_dim, a.max_positions, device)
+            self.qf = torch.empty((m, s.hidden), **f32)
+            self.kf = torch.empty((m, s.kv_dim), **f32)
+            self.vf = torch.empty((m, s.kv_dim), **f32)
+            self.xn = torch.empty((m, s.hidden), **b16)
+            self.att = torch.empty((m, s.hidden), **b16)
 
     def run(self) -> torch.Tensor:
+        if self.attn is not None:
+            return self._run_full()
         s = self.ls.shape
         self.h.copy_(self.x_in)
         self.h_bf16.copy_(self.x_in)
@@ -132,6 +184,32 @@ class DecodeStep:
             gguf_gemv_residual(self.s, d.data, d.ggml_type, d.shape, self.h, self.h_bf16)
         w = self.ls.lm_head
         gguf_gemv(self.h_bf16, w.data, w.ggml_type, w.shape, out=self.logits)
+        return self.logits
+
+    def _run_full(self) -> torch.Tensor:
+        s, a = self.ls.shape, self.attn
+        self.h.copy_(self.x_in)
+        for li, layer in enumerate(self.ls.layers):
+            norms = self.ls.norms[li]
+            rms_norm(self.h, norms["attn"], a.rms_eps, out_bf16=self.xn)
+            q, k, v, o = layer["q"], layer["k"], layer["v"], layer["o"]
+            if q.ggml_type == k.ggml_type == v.ggml_type:
+                gguf_gemv_multi(self.xn, [(q.data, q.shape[0]), (k.data, k.shape[0]), (v.data, v.shape[0])],
+                                q.ggml_type, s.hidden, [self.qf, self.kf, self.vf])
+            else:
+                for w, out in ((q, self.qf), (k, self.kf), (v, self.vf)):
+                    gguf_gemv_multi(self.xn, [(w.data, w.shape[0])], w.ggml_type, s.hidden, [out])
+            decode_attention(self.qf, self.kf, self.vf, self.k_cache[li], self.v_cache[li], self.positions,
+                             a.n_heads, a.n_kv_heads, rope=self.rope, out=self.att, workspace=self.ws)
+            gguf_gemv_residual(self.att, o.data, o.ggml_type, o.shape, self.h)
+            rms_norm(self.h, norms["ffn"], a.rms_eps, out_bf16=self.xn)
+            g, u, d = layer["gate"], layer["up"], layer["down"]
+            gguf_gemv_swiglu(self.xn, g.data, u.data, g.ggml_type, g.shape, out_bf16=self.s)
+            gguf_gemv_residual(self.s, d.data, d.ggml_type, d.shape, self.h)
+        rms_norm(self.h, self.ls.output_norm, a.rms_eps, out_bf16=self.xn)
+        w = self.ls.lm_head
+        gguf_gemv(self.xn, w.data, w.ggml_type, w.shape, out=self.logits)
+        self.positions.add_(1)
         return self.logits
 
     def capture(self) -> None:

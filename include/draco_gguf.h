@@ -200,9 +200,8 @@ int draco_gguf_rms_norm(const float* x, const float* weight, float eps, float* y
                         void* stream);
 
 /*
- * Workspace bytes draco_gguf_decode_attention needs (0 for invalid sizes).
- * The workspace must be zeroed before its first use; the kernel leaves it
- * ready for the next call.
+ * Workspace bytes draco_gguf_decode_attention needs (0 for invalid sizes):
+ * the partial softmax states of the position splits.
  */
 size_t draco_gguf_decode_attention_workspace_size(int64_t batch, int n_q_heads, int n_kv_heads, int head_dim,
                                                   int64_t max_positions);
@@ -219,8 +218,10 @@ size_t draco_gguf_decode_attention_workspace_size(int64_t batch, int n_q_heads, 
  * sequence (query head h reads kv head h / (n_q_heads / n_kv_heads);
  * scores q.k / sqrt(head_dim), softmax, weighted sum of v) to out
  * [b, n_q_heads * head_dim], float32 or bfloat16 (out_dtype).  head_dim 64
- * or 128, up to 8 query heads per kv head.  A position outside
- * [0, max_positions) touches no cache memory and yields NaN outputs.
+ * or 128, 1, 2, 4 or 8 query heads per kv head, max_positions <= 131072.
+ * Two launches: partial attention per 256-position split, then the merge.
+ * A position outside [0, max_positions) touches no cache memory and yields
+ * NaN outputs.
  * Replaces apply_rope (draco/runtime/cpu/ops.py:73-92) on q / k and
  * CPUAttentionBackend.decode (draco/runtime/cpu/attention.py:35-81) with its
  * CPUKVCache append (float16 storage, draco/runtime/cpu/kv_cache.py:19-28).

@@ -77,7 +77,7 @@ def test_decode_attention_llama_heads(positions):
     _attention_case(len(positions), 32, 8, 128, 1024, positions, 500000.0, True, seed=sum(positions) + 1)
 
 
-@pytest.mark.parametrize("hq,hkv,d,rope", [(8, 8, 64, True), (16, 2, 64, False), (12, 4, 128, True)])
+@pytest.mark.parametrize("hq,hkv,d,rope", [(8, 8, 64, True), (16, 2, 64, False), (16, 8, 128, True), (64, 8, 128, True)])
 def test_decode_attention_shapes(hq, hkv, d, rope):
     print(f"decode attention hq={hq} hkv={hkv} d={d} rope={rope}", flush=True)
     _attention_case(3, hq, hkv, d, 600, [0, 299, 599], 10000.0, rope, seed=hq + d)

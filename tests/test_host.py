@@ -241,3 +241,23 @@ def test_quantizers_round_trip(qtype, tol):
     deq = gguf_ref.dequantize_matrix(qtype, b, w.shape)
     rms = np.sqrt(np.mean((deq - w) ** 2)) / np.sqrt(np.mean(w ** 2))
     assert rms < tol, (qtype, rms)
+
+
+def test_decode_glue_validation_before_launch():
+    """Shape and pointer checks of the glue entry points fail before any launch."""
+    lib = _native.load()
+    ws = lib.draco_gguf_decode_attention_workspace_size(1, 32, 8, 128, 1024)
+    assert ws > 0
+    assert lib.draco_gguf_decode_attention_workspace_size(1, 12, 8, 128, 1024) == 0  # not a multiple
+    args = dict(q=FAKE, k=FAKE, v=FAKE, kc=FAKE, vc=FAKE, pos=FAKE)
+
+    def call(hq, hkv, d, max_pos, ws_bytes=1 << 30, cos=None, sin=None):
+        return lib.draco_gguf_decode_attention(args["q"], args["k"], args["v"], args["kc"], args["vc"], args["pos"],
+                                               1, hq, hkv, d, max_pos, cos, sin, FAKE, 0, FAKE, ws_bytes, None)
+    assert call(12, 4, 128, 64) == _native.DRACO_EINVAL_SHAPE     # 3 query heads per kv head
+    assert call(32, 8, 96, 64) == _native.DRACO_EINVAL_SHAPE      # head_dim
+    assert call(32, 8, 128, 1 << 25) == _native.DRACO_EINVAL_SHAPE
+    assert call(32, 8, 128, 64, cos=FAKE) == _native.DRACO_EINVAL_ARG
+    assert call(32, 8, 128, 64, ws_bytes=16) == _native.DRACO_EWORKSPACE
+    assert lib.draco_gguf_rms_norm(FAKE, FAKE, 1e-5, FAKE, None, 1, 6, None) == _native.DRACO_EINVAL_SHAPE
+    assert lib.draco_gguf_rms_norm(FAKE, FAKE, 1e-5, None, None, 1, 8, None) == _native.DRACO_EINVAL_ARG

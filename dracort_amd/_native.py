@@ -59,6 +59,14 @@ SIGNATURES = {
         [_c_int, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp), _c_size, _vp, _vp, _c_int, _vp,
          _c_i64, _c_i64, _c_i64, _c_int, _c_int, _vp, _c_size, _vp],
     ),
+    "draco_gguf_gemv_multi_rmsnorm": (
+        _c_int,
+        [_c_int, _c_int, ctypes.POINTER(_vp), ctypes.POINTER(_c_size), ctypes.POINTER(_c_i64), ctypes.POINTER(_vp),
+         ctypes.POINTER(_vp), _vp, _vp, ctypes.c_float, _vp, _c_i64, _c_i64, _vp],
+    ),
+    "draco_gguf_gemv_swiglu_rmsnorm": (
+        _c_int, [_c_int, _vp, _vp, _c_size, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]
+    ),
     "draco_gguf_rms_norm": (_c_int, [_vp, _vp, ctypes.c_float, _vp, _vp, _c_i64, _c_i64, _vp]),
     "draco_gguf_decode_attention_workspace_size": (_c_size, [_c_i64, _c_int, _c_int, _c_int, _c_i64]),
     "draco_gguf_decode_attention": (

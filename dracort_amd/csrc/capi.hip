@@ -232,6 +232,80 @@ int draco_gguf_gemv_residual(int ggml_type, const void* w, size_t w_bytes, const
                              static_cast<hipStream_t>(stream));
 }
 
+// shared checks of the fused-RMSNorm entry points: x [m, k] float32, norm_w [k], x_norm [m, k] bf16
+static int check_norm_args(const float* x, const float* norm_w, float eps, const void* x_norm, int64_t m, int64_t k) {
+  if (int rc = check_ptr(x, "x")) return rc;
+  if (int rc = check_ptr(norm_w, "norm_w")) return rc;
+  if (int rc = check_ptr(x_norm, "x_norm")) return rc;
+  if (!(eps >= 0.f)) return set_error(DRACO_EINVAL_ARG, "eps must be >= 0");
+  if (overlaps(x, (size_t)m * k * 4, x_norm, (size_t)m * k * 2)) return set_error(DRACO_EINVAL_ARG, "x_norm overlaps x");
+  return DRACO_OK;
+}
+
+int draco_gguf_gemv_multi_rmsnorm(int ggml_type, int n_mats, const void* const* w, const size_t* w_bytes,
+                                  const int64_t* n, float* const* y, void* const* y_bf16, const float* x,
+                                  const float* norm_w, float eps, void* x_norm, int64_t m, int64_t k, void* stream) {
+  g_last_error[0] = 0;
+  TypeInfo t;
+  if (int rc = decode_type(ggml_type, &t)) return rc;
+  if (n_mats < 1 || n_mats > 4) return set_error(DRACO_EINVAL_ARG, "n_mats must be 1..4, got %d", n_mats);
+  if (!w || !w_bytes || !n) return set_error(DRACO_EINVAL_ARG, "w, w_bytes and n must not be NULL");
+  if (m < 1 || m > 16)
+    return set_error(DRACO_EINVAL_SHAPE, "GEMV takes 1..16 activation rows, got %lld", (long long)m);
+  if (int rc = check_norm_args(x, norm_w, eps, x_norm, m, k)) return rc;
+  int ns[4];
+  int64_t total = 0;
+  float* ys[4] = {nullptr, nullptr, nullptr, nullptr};
+  uint16_t* ybs[4] = {nullptr, nullptr, nullptr, nullptr};
+  for (int i = 0; i < n_mats; ++i) {
+    if (int rc = check_matrix(t, n[i], k)) return rc;
+    if (int rc = check_bytes(t, n[i], k, w_bytes[i], "w[i]")) return rc;
+    if (int rc = check_ptr(w[i], "w[i]")) return rc;
+    ys[i] = y ? y[i] : nullptr;
+    ybs[i] = y_bf16 ? static_cast<uint16_t*>(y_bf16[i]) : nullptr;
+    if (!ys[i] && !ybs[i]) return set_error(DRACO_EINVAL_ARG, "matrix %d has neither y nor y_bf16", i);
+    if (ys[i] && (reinterpret_cast<uintptr_t>(ys[i]) & 3u)) return set_error(DRACO_EINVAL_ARG, "y[%d] misaligned", i);
+    if (ybs[i] && (reinterpret_cast<uintptr_t>(ybs[i]) & 1u))
+      return set_error(DRACO_EINVAL_ARG, "y_bf16[%d] misaligned", i);
+    for (const void* in : {static_cast<const void*>(x), static_cast<const void*>(x_norm)}) {
+      const size_t nb = in == x ? (size_t)m * k * 4 : (size_t)m * k * 2;
+      if (overlaps(in, nb, ys[i], (size_t)m * n[i] * 4) || overlaps(in, nb, ybs[i], (size_t)m * n[i] * 2))
+        return set_error(DRACO_EINVAL_ARG, "x or x_norm overlaps an output of matrix %d", i);
+    }
+    ns[i] = (int)n[i];
+    total += n[i];
+  }
+  if (total > kMaxDim) return set_error(DRACO_EINVAL_SHAPE, "too many rows in one launch");
+  return gemv_multi_norm_dispatch(t.base, t.d_last, n_mats, w, ns, ys, ybs, x, norm_w, eps,
+                                  static_cast<uint16_t*>(x_norm), (int)m, (int)k, static_cast<hipStream_t>(stream));
+}
+
+int draco_gguf_gemv_swiglu_rmsnorm(int ggml_type, const void* w_gate, const void* w_up, size_t w_bytes,
+                                   const float* x, const float* norm_w, float eps, void* x_norm, float* y,
+                                   void* y_bf16, int64_t m, int64_t n, int64_t k, void* stream) {
+  g_last_error[0] = 0;
+  TypeInfo t;
+  if (int rc = decode_type(ggml_type, &t)) return rc;
+  if (int rc = check_matrix(t, n, k)) return rc;
+  if (int rc = check_bytes(t, n, k, w_bytes, "w")) return rc;
+  if (m < 1 || m > 16)
+    return set_error(DRACO_EINVAL_SHAPE, "GEMV takes 1..16 activation rows, got %lld", (long long)m);
+  if (int rc = check_ptr(w_gate, "w_gate")) return rc;
+  if (int rc = check_ptr(w_up, "w_up")) return rc;
+  if (int rc = check_norm_args(x, norm_w, eps, x_norm, m, k)) return rc;
+  if (!y && !y_bf16) return set_error(DRACO_EINVAL_ARG, "y and y_bf16 are both NULL");
+  if ((reinterpret_cast<uintptr_t>(y) & 3u) || (reinterpret_cast<uintptr_t>(y_bf16) & 1u))
+    return set_error(DRACO_EINVAL_ARG, "y / y_bf16 misaligned");
+  for (const void* in : {static_cast<const void*>(x), static_cast<const void*>(x_norm)}) {
+    const size_t nb = in == x ? (size_t)m * k * 4 : (size_t)m * k * 2;
+    if (overlaps(in, nb, y, (size_t)m * n * 4) || overlaps(in, nb, y_bf16, (size_t)m * n * 2))
+      return set_error(DRACO_EINVAL_ARG, "x or x_norm overlaps an output");
+  }
+  return gemv_swiglu_norm_dispatch(t.base, t.d_last, w_gate, w_up, y, static_cast<uint16_t*>(y_bf16), x, norm_w, eps,
+                                   static_cast<uint16_t*>(x_norm), (int)m, (int)n, (int)k,
+                                   static_cast<hipStream_t>(stream));
+}
+
 size_t draco_gguf_gemm_workspace_size(int ggml_type, int64_t m, int64_t k) {
   TypeInfo t;
   if (decode_type(ggml_type, &t) || m < 1 || k < 1) return 0;

@@ -31,6 +31,22 @@ int gemv_swiglu_dispatch(int qtype, bool d_last, const void* w_gate, const void*
 int gemv_resid_dispatch(int qtype, bool d_last, const void* w, const void* x, bool xbf16, float* resid,
                         uint16_t* resid_bf16, int m, int n, int k, hipStream_t s);
 
+// RMSNorm of m rows of n float32 values into float32 y and / or bf16 yb.
+int rms_norm_launch(const float* x, const float* w, float eps, float* y, uint16_t* yb, int64_t m, int64_t n,
+                    hipStream_t s);
+
+// GEMV launches whose input is RMSNorm(x) (x float32 [m, k]): fused into the
+// persistent single-token kernel where it runs, else rms_norm_launch into
+// x_norm followed by the plain launch.  x_norm [m, k] bf16 always receives the
+// normalized input.
+int gemv_multi_norm_dispatch(int qtype, bool d_last, int n_mats, const void* const* w, const int* n, float* const* y,
+                             uint16_t* const* yb, const float* x, const float* norm_w, float eps, uint16_t* x_norm,
+                             int m, int k, hipStream_t s);
+
+int gemv_swiglu_norm_dispatch(int qtype, bool d_last, const void* w_gate, const void* w_up, float* y, uint16_t* yb,
+                              const float* x, const float* norm_w, float eps, uint16_t* x_norm, int m, int n, int k,
+                              hipStream_t s);
+
 // Workspace bytes of the GEMM of this base type (0: it needs none).
 size_t gemm_workspace_size(int qtype, int64_t m, int64_t k);
 

@@ -52,6 +52,17 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return v;
 }
 
+// Sum over a 256-thread workgroup (4 waves), result in every thread; red:
+// 4 floats of LDS.  Every thread must call it (two barriers).
+__device__ __forceinline__ float block_sum_256(float v, float* red) {
+  v = wave_sum_dpp(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
 

@@ -50,6 +50,12 @@ struct StreamJob {
   const float* bias;  // kPlain with one matrix only
   float* resid;
   uint16_t* resid_bf16;
+  // fused RMSNorm of the input (persistent single-token kernels only): x is
+  // float32, normalized with norm_w / norm_eps in the prologue; workgroup 0
+  // also stores the normalized bf16 row to x_norm
+  const float* norm_w;
+  float norm_eps;
+  uint16_t* x_norm;
 };
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {

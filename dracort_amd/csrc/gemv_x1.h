@@ -204,6 +204,52 @@ __device__ __forceinline__ void x1_fetch_x(const void* __restrict__ x, int k, ui
   for (int j = 0; j < XC; ++j) xr[j] = xs[min((int)threadIdx.x + 256 * j, chunks - 1)];
 }
 
+// The same two chunks from a float32 row h with the RMSNorm applied:
+// y = h / sqrt(mean(h^2) + eps) * w, rounded to bf16 (draco/runtime/cpu/ops.py:15-19).
+// red: 4 floats of LDS outside the activation image; every thread of the
+// workgroup calls this (the sum of squares is a workgroup reduction).
+// Workgroup 0 also stores the normalized row to x_norm (if not NULL).
+__device__ __forceinline__ void x1_fetch_x_rmsnorm(const float* __restrict__ h, const float* __restrict__ w,
+                                                   float eps, uint16_t* x_norm, int k, float* red, uint4 (&xr)[2]) {
+  const int chunks = k >> 3;
+  const float4* h4 = reinterpret_cast<const float4*>(h);
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  float4 v[4], g[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = min((int)threadIdx.x + 256 * j, chunks - 1);
+    v[2 * j] = h4[2 * c];
+    v[2 * j + 1] = h4[2 * c + 1];
+    g[2 * j] = w4[2 * c];
+    g[2 * j + 1] = w4[2 * c + 1];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if ((int)threadIdx.x + 256 * j < chunks) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const float4 a = v[2 * j + q];
+        ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+      }
+    }
+  }
+  const float denom = sqrtf(block_sum_256(ss, red) / (float)k + eps);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    uint32_t pk[4];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float4 a = v[2 * j + q], b = g[2 * j + q];
+      pk[2 * q] = f32_to_bf16_rne(a.x / denom * b.x) | ((uint32_t)f32_to_bf16_rne(a.y / denom * b.y) << 16);
+      pk[2 * q + 1] = f32_to_bf16_rne(a.z / denom * b.z) | ((uint32_t)f32_to_bf16_rne(a.w / denom * b.w) << 16);
+    }
+    xr[j] = uint4{pk[0], pk[1], pk[2], pk[3]};
+    const int c = (int)threadIdx.x + 256 * j;
+    if (x_norm && blockIdx.x == 0 && c < chunks) reinterpret_cast<uint4*>(x_norm)[c] = xr[j];
+  }
+}
+
 template <int QT, int XC>
 __device__ __forceinline__ void x1_stage_regs(uint4* lds, const uint4 (&xr)[XC], int k) {
   const int chunks = k >> 3;
@@ -473,7 +519,7 @@ struct X1Rows {
 // before it multiplies row i; results are kept in lane i % 64 of one register
 // and stored after every 64 rows, so no store sits between the loads.  The
 // activations (the bf16 LDS image) are read into registers once.
-template <int QT, bool DL, int MODE, int PF>
+template <int QT, bool DL, int MODE, int PF, bool NORM = false>
 __global__ __launch_bounds__(256) void gemv_x1p_kernel(StreamJob job) {
   constexpr int NR = MODE == kSwiGLU ? 2 : 1;
   constexpr int NB = PF + 1;
@@ -488,12 +534,17 @@ __global__ __launch_bounds__(256) void gemv_x1p_kernel(StreamJob job) {
 
   // 1. activations (two 16-byte chunks per thread), then the first rows
   uint4 xr[2];
-  x1_fetch_x<2>(job.x, k, xr);
+  if constexpr (!NORM) x1_fetch_x<2>(job.x, k, xr);
   X1Raw<QT> buf[NB][NR];
 #pragma unroll
   for (int p = 0; p < PF; ++p)
 #pragma unroll
     for (int q = 0; q < NR; ++q) buf[p][q] = x1_load<QT, DL>(rows.buf(job, p, q), ul);
+  if constexpr (NORM) {
+    // the row's RMSNorm (a workgroup reduction) after the first weight loads are out
+    float* red = reinterpret_cast<float*>(x1_smem + x1p_lds_bytes(QT, k) / 16);
+    x1_fetch_x_rmsnorm(static_cast<const float*>(job.x), job.norm_w, job.norm_eps, job.x_norm, k, red, xr);
+  }
 
   // 2. the LDS image and group sums; the lane's activations into registers
   x1_stage_regs<QT, 2>(x1_smem, xr, k);
@@ -525,13 +576,13 @@ __global__ __launch_bounds__(256) void gemv_x1p_kernel(StreamJob job) {
   if (nrow & 63) rows.flush(job, nrow & ~63, nrow & 63, res);
 }
 
-template <int QT, bool DL, int MODE, int PF>
+template <int QT, bool DL, int MODE, int PF, bool NORM = false>
 static int launch_x1p(const StreamJob& job, int blocks_per_cu, hipStream_t s) {
   if (job.k > 4096 || job.k % 256 != 0) return set_error(DRACO_EINVAL_SHAPE, "persistent GEMV takes K <= 4096");
-  const size_t lds = x1p_lds_bytes(QT, job.k);
+  const size_t lds = x1p_lds_bytes(QT, job.k) + (NORM ? 16 : 0);
   const int need = (job.rows + 3) / 4;
   const int blocks = std::max(1, std::min(need, device_cus() * blocks_per_cu));
-  hipLaunchKernelGGL((gemv_x1p_kernel<QT, DL, MODE, PF>), dim3(blocks), dim3(256), lds, s, job);
+  hipLaunchKernelGGL((gemv_x1p_kernel<QT, DL, MODE, PF, NORM>), dim3(blocks), dim3(256), lds, s, job);
   return check_launch("gemv_x1p");
 }
 
@@ -705,6 +756,24 @@ namespace draco {
 // form is compiled with predicated loads (ALLOW_FULL = false): letting the
 // compiler interleave each row's loads with the previous row's math was
 // measured faster than hoisting every load of the step.
+// Whether the persistent single-token kernel runs this launch (and so can
+// take the fused RMSNorm prologue).
+inline bool x1p_ok(int qtype, const StreamJob& job, bool xbf16) {
+  if (!(job.m == 1 && xbf16 && (qtype == kQ4_K || qtype == kQ6_K) && job.k <= 4096)) return false;
+  for (int i = 0; i < job.n_mats; ++i)
+    if ((int64_t)job.n[i] * job.row_bytes >= ((int64_t)1 << 31)) return false;
+  return true;
+}
+
+// The fused-RMSNorm launch (job.x float32, job.norm_w set); x1p_ok must hold.
+template <int MODE>
+static int gemv_dispatch_norm(int qtype, bool d_last, const StreamJob& job, hipStream_t s) {
+  const int bpc = job.rows >= 8192 ? 4 : 3;
+  if (qtype == kQ4_K) return launch_x1p<kQ4_K, false, MODE, 1, true>(job, bpc, s);
+  return d_last ? launch_x1p<kQ6_K, true, MODE, 1, true>(job, bpc, s)
+                : launch_x1p<kQ6_K, false, MODE, 1, true>(job, bpc, s);
+}
+
 template <int MODE>
 static int gemv_dispatch_mode(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s) {
   bool x1 = job.m == 1 && xbf16 && (qtype == kQ4_K || qtype == kQ6_K);

@@ -31,15 +31,6 @@
 
 namespace draco {
 
-__device__ __forceinline__ float block_sum_256(float v, float* red) {
-  v = wave_sum_dpp(v);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  return red[0] + red[1] + red[2] + red[3];
-}
-
 // Max over the 64 lanes, result in every lane (DPP within rows of 16, then two exchanges).
 __device__ __forceinline__ float wave_max_dpp(float v) {
   v = fmaxf(v, dpp_f<0xB1>(v));

@@ -14,8 +14,10 @@ from dracort_amd.kernels.gguf import (  # noqa: F401
     gguf_gemm,
     gguf_gemv,
     gguf_gemv_multi,
+    gguf_gemv_multi_rmsnorm,
     gguf_gemv_residual,
     gguf_gemv_swiglu,
+    gguf_gemv_swiglu_rmsnorm,
     gguf_linear,
     gguf_moe,
     moe_workspace_bytes,
@@ -27,6 +29,8 @@ __all__ = [
     "gguf_gemv",
     "gguf_gemv_multi",
     "gguf_gemv_swiglu",
+    "gguf_gemv_multi_rmsnorm",
+    "gguf_gemv_swiglu_rmsnorm",
     "gguf_gemv_residual",
     "gguf_gemm",
     "gguf_moe",

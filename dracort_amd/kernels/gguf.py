@@ -312,6 +312,93 @@ def gguf_gemv_residual(
     _native.check(rc, "gguf_gemv_residual")
 
 
+def _norm_args(x: torch.Tensor, norm_weight: torch.Tensor, x_norm: torch.Tensor, k: int) -> int:
+    _need_gpu(x, "x")
+    _need_gpu(norm_weight, "norm_weight")
+    _need_gpu(x_norm, "x_norm")
+    if x.dtype != torch.float32 or norm_weight.dtype != torch.float32:
+        raise ValueError("fused RMSNorm takes float32 x and norm_weight")
+    if x.numel() % k or tuple(norm_weight.shape) != (k,):
+        raise ValueError(f"x must be [m, {k}] and norm_weight [{k}]")
+    m = x.numel() // k
+    if x_norm.dtype != torch.bfloat16 or x_norm.numel() != m * k:
+        raise ValueError(f"x_norm must be bfloat16 [{m}, {k}]")
+    _same_device(x, norm_weight, x_norm)
+    return m
+
+
+def gguf_gemv_multi_rmsnorm(
+    x: torch.Tensor,
+    norm_weight: torch.Tensor,
+    eps: float,
+    x_norm: torch.Tensor,
+    weights: Sequence[Tuple[torch.Tensor, int]],
+    ggml_type: int,
+    k: int,
+    outs: Sequence[Optional[torch.Tensor]],
+    outs_bf16: Optional[Sequence[Optional[torch.Tensor]]] = None,
+) -> None:
+    """``gguf_gemv_multi`` on ``x_norm = bf16(rms_norm(x, norm_weight, eps))`` (x float32
+    [m, k]; x_norm is written).  The norm runs in the GEMV's prologue where the
+    persistent single-token kernel applies, else as its own launch."""
+    m = _norm_args(x, norm_weight, x_norm, k)
+    nm = len(weights)
+    if not 1 <= nm <= 4 or len(outs) != nm or (outs_bf16 is not None and len(outs_bf16) != nm):
+        raise ValueError("1..4 weights with one output slot each")
+    outs_bf16 = list(outs_bf16) if outs_bf16 is not None else [None] * nm
+    for i, (q, n) in enumerate(weights):
+        _check_weight(q, ggml_type, (n, k))
+        _same_device(x, q)
+        if outs[i] is None and outs_bf16[i] is None:
+            raise ValueError(f"weight {i} has no output")
+        _out_check(outs[i], torch.float32, m * n, f"outs[{i}]")
+        _out_check(outs_bf16[i], torch.bfloat16, m * n, f"outs_bf16[{i}]")
+    vp = ctypes.c_void_p
+    w_arr = (vp * nm)(*[q.data_ptr() for q, _ in weights])
+    b_arr = (ctypes.c_size_t * nm)(*[q.numel() for q, _ in weights])
+    n_arr = (ctypes.c_int64 * nm)(*[int(n) for _, n in weights])
+    y_arr = (vp * nm)(*[o.data_ptr() if o is not None else None for o in outs])
+    yb_arr = (vp * nm)(*[o.data_ptr() if o is not None else None for o in outs_bf16])
+    lib = _native.load()
+    with torch.cuda.device(x.device):
+        rc = lib.draco_gguf_gemv_multi_rmsnorm(int(ggml_type), nm, w_arr, b_arr, n_arr, y_arr, yb_arr, x.data_ptr(),
+                                               norm_weight.data_ptr(), float(eps), x_norm.data_ptr(), m, k,
+                                               _stream(x))
+    _native.check(rc, "gguf_gemv_multi_rmsnorm")
+
+
+def gguf_gemv_swiglu_rmsnorm(
+    x: torch.Tensor,
+    norm_weight: torch.Tensor,
+    eps: float,
+    x_norm: torch.Tensor,
+    w_gate: torch.Tensor,
+    w_up: torch.Tensor,
+    ggml_type: int,
+    shape: Tuple[int, int],
+    out: Optional[torch.Tensor] = None,
+    out_bf16: Optional[torch.Tensor] = None,
+) -> None:
+    """``gguf_gemv_swiglu`` on ``x_norm = bf16(rms_norm(x, norm_weight, eps))``."""
+    n, k = _check_weight(w_gate, ggml_type, shape)
+    _check_weight(w_up, ggml_type, shape)
+    if w_gate.numel() != w_up.numel():
+        raise ValueError("gate and up buffers differ in size")
+    m = _norm_args(x, norm_weight, x_norm, k)
+    if out is None and out_bf16 is None:
+        raise ValueError("need out and/or out_bf16")
+    _out_check(out, torch.float32, m * n, "out")
+    _out_check(out_bf16, torch.bfloat16, m * n, "out_bf16")
+    _same_device(x, w_gate, w_up)
+    lib = _native.load()
+    with torch.cuda.device(x.device):
+        rc = lib.draco_gguf_gemv_swiglu_rmsnorm(
+            int(ggml_type), w_gate.data_ptr(), w_up.data_ptr(), w_gate.numel(), x.data_ptr(), norm_weight.data_ptr(),
+            float(eps), x_norm.data_ptr(), out.data_ptr() if out is not None else None,
+            out_bf16.data_ptr() if out_bf16 is not None else None, m, n, k, _stream(x))
+    _native.check(rc, "gguf_gemv_swiglu_rmsnorm")
+
+
 def moe_workspace_bytes(tokens: int, hidden: int, inter: int, n_experts: int, top_k: int) -> int:
     return int(_native.load().draco_gguf_moe_workspace_size(tokens, hidden, inter, n_experts, top_k))
 

@@ -33,7 +33,14 @@ import torch
 
 from dracort_amd.format.gguf import GGML_TYPE_Q4_K, GGML_TYPE_Q6_K, tensor_bytes
 from dracort_amd.kernels.glue import DecodeAttentionWorkspace, decode_attention, rms_norm, rope_tables
-from dracort_amd.kernels.gguf import gguf_gemv, gguf_gemv_multi, gguf_gemv_residual, gguf_gemv_swiglu
+from dracort_amd.kernels.gguf import (
+    gguf_gemv,
+    gguf_gemv_multi,
+    gguf_gemv_multi_rmsnorm,
+    gguf_gemv_residual,
+    gguf_gemv_swiglu,
+    gguf_gemv_swiglu_rmsnorm,
+)
 from dracort_amd.quantization.gguf import GGUFQuantizedWeight
 from dracort_amd.quantization.quantize import quantize
 
@@ -191,24 +198,26 @@ class DecodeStep:
         self.h.copy_(self.x_in)
         for li, layer in enumerate(self.ls.layers):
             norms = self.ls.norms[li]
-            rms_norm(self.h, norms["attn"], a.rms_eps, out_bf16=self.xn)
             q, k, v, o = layer["q"], layer["k"], layer["v"], layer["o"]
             if q.ggml_type == k.ggml_type == v.ggml_type:
-                gguf_gemv_multi(self.xn, [(q.data, q.shape[0]), (k.data, k.shape[0]), (v.data, v.shape[0])],
-                                q.ggml_type, s.hidden, [self.qf, self.kf, self.vf])
+                # the attention norm runs in the q/k/v launch's prologue
+                gguf_gemv_multi_rmsnorm(self.h, norms["attn"], a.rms_eps, self.xn,
+                                        [(q.data, q.shape[0]), (k.data, k.shape[0]), (v.data, v.shape[0])],
+                                        q.ggml_type, s.hidden, [self.qf, self.kf, self.vf])
             else:
+                rms_norm(self.h, norms["attn"], a.rms_eps, out_bf16=self.xn)
                 for w, out in ((q, self.qf), (k, self.kf), (v, self.vf)):
                     gguf_gemv_multi(self.xn, [(w.data, w.shape[0])], w.ggml_type, s.hidden, [out])
             decode_attention(self.qf, self.kf, self.vf, self.k_cache[li], self.v_cache[li], self.positions,
                              a.n_heads, a.n_kv_heads, rope=self.rope, out=self.att, workspace=self.ws)
             gguf_gemv_residual(self.att, o.data, o.ggml_type, o.shape, self.h)
-            rms_norm(self.h, norms["ffn"], a.rms_eps, out_bf16=self.xn)
             g, u, d = layer["gate"], layer["up"], layer["down"]
-            gguf_gemv_swiglu(self.xn, g.data, u.data, g.ggml_type, g.shape, out_bf16=self.s)
+            gguf_gemv_swiglu_rmsnorm(self.h, norms["ffn"], a.rms_eps, self.xn, g.data, u.data, g.ggml_type, g.shape,
+                                     out_bf16=self.s)
             gguf_gemv_residual(self.s, d.data, d.ggml_type, d.shape, self.h)
-        rms_norm(self.h, self.ls.output_norm, a.rms_eps, out_bf16=self.xn)
         w = self.ls.lm_head
-        gguf_gemv(self.xn, w.data, w.ggml_type, w.shape, out=self.logits)
+        gguf_gemv_multi_rmsnorm(self.h, self.ls.output_norm, a.rms_eps, self.xn, [(w.data, w.shape[0])],
+                                w.ggml_type, s.hidden, [self.logits])
         self.positions.add_(1)
         return self.logits
 

@@ -190,6 +190,23 @@ int draco_gguf_moe_ffn(int ggml_type, const void* const* w_gate, const void* con
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * draco_gguf_gemv_multi / draco_gguf_gemv_swiglu whose input is
+ * RMSNorm(x): x [m, k] float32, norm_w [k] float32,
+ *   x_norm = bf16(x / sqrt(mean(x^2) + eps) * norm_w)   ([m, k], written)
+ * and the GEMV runs on x_norm.  For single-token bf16-eligible launches of
+ * Q4_K / Q6_K (k <= 4096) the norm runs in the GEMV's own prologue (no extra
+ * launch); otherwise it is a separate RMSNorm launch.  Replaces _norm
+ * (draco/runtime/cpu/executor.py:199-206) followed by _qkv / _mlp.
+ */
+int draco_gguf_gemv_multi_rmsnorm(int ggml_type, int n_mats, const void* const* w, const size_t* w_bytes,
+                                  const int64_t* n, float* const* y, void* const* y_bf16, const float* x,
+                                  const float* norm_w, float eps, void* x_norm, int64_t m, int64_t k, void* stream);
+
+int draco_gguf_gemv_swiglu_rmsnorm(int ggml_type, const void* w_gate, const void* w_up, size_t w_bytes,
+                                   const float* x, const float* norm_w, float eps, void* x_norm, float* y,
+                                   void* y_bf16, int64_t m, int64_t n, int64_t k, void* stream);
+
+/*
  * RMSNorm of m rows of n float32 values (n a multiple of 4):
  *   y[r, i] = x[r, i] / sqrt(mean_j(x[r, j]^2) + eps) * weight[i]
  * into float32 y and / or bfloat16 y_bf16 (either may be NULL, not both).

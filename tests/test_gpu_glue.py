@@ -123,3 +123,42 @@ def test_decode_attention_sequence_of_steps_reuses_workspace():
                                        s[0].astype(np.float64))
             ref = decode_ref.decode_attention_f64(qq, kc_gpu[i], vc_gpu[i], pos[i] + 1)
             check_close(out[i].reshape(hq, d), ref, f"step {step} b={i}")
+
+
+@pytest.mark.parametrize("qtype,m", [(12, 1), (14, 1), (12, 3), (3, 1)])
+def test_fused_rmsnorm_gemv_matches_norm_then_gemv(qtype, m):
+    """The RMSNorm in the GEMV prologue (Q4_K / Q6_K, one token) or as its own
+    launch (other cases): x_norm within one bf16 ulp of the standalone norm,
+    outputs within the matmul bar of the fp64 product of that x_norm."""
+    from dracort_amd.kernels import gguf_gemv_multi_rmsnorm, gguf_gemv_swiglu_rmsnorm
+    from oracle import matmul_ref
+    from tests.gguf_cases import quantized
+
+    k = 4096 if qtype != 3 else 1024
+    rng = np.random.default_rng(qtype + m)
+    x = (rng.standard_normal((m, k)) * 2).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    xd, wd = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    ref_norm = torch.empty((m, k), dtype=torch.bfloat16, device="cuda")
+    rms_norm(xd, wd, 1e-5, out_bf16=ref_norm)
+    mats = [quantized(qtype, n, k, seed=n) for n in (512, 256)]
+    outs = [torch.empty((m, n), device="cuda") for n in (512, 256)]
+    xn = torch.empty((m, k), dtype=torch.bfloat16, device="cuda")
+    print(f"fused rmsnorm multi type {qtype} m={m}", flush=True)
+    gguf_gemv_multi_rmsnorm(xd, wd, 1e-5, xn, [(torch.from_numpy(b).cuda(), wt.shape[0]) for b, wt in mats], qtype, k,
+                            outs)
+    a, r = xn.float().cpu().numpy(), ref_norm.float().cpu().numpy()
+    ulp = np.abs(np.spacing(r.astype(np.float32))) * 2 ** 16  # one bf16 ulp
+    assert np.all(np.abs(a - r) <= ulp) and np.mean(a == r) > 0.99
+    xs = xn.float().cpu().numpy()
+    for (b, wt), y in zip(mats, outs):
+        check_close(y.cpu().numpy(), matmul_ref.linear_ref(xs, wt), f"fused norm multi {qtype} m={m}")
+    gb, gw = quantized(qtype, 1024, k, seed=5)
+    ub, uw = quantized(qtype, 1024, k, seed=6)
+    y = torch.empty((m, 1024), device="cuda")
+    print(f"fused rmsnorm swiglu type {qtype} m={m}", flush=True)
+    gguf_gemv_swiglu_rmsnorm(xd, wd, 1e-5, xn, torch.from_numpy(gb).cuda(), torch.from_numpy(ub).cuda(), qtype,
+                             (1024, k), out=y)
+    xs = xn.float().cpu().numpy()
+    g = matmul_ref.linear_ref(xs, gw)
+    check_close(y.cpu().numpy(), g / (1 + np.exp(-g)) * matmul_ref.linear_ref(xs, uw), f"fused norm swiglu {qtype}")

@@ -11,18 +11,19 @@
 //   * cache layout [batch][kv head][position][head_dim] float16 (head-major:
 //     a head's keys are consecutive, so a workgroup's key reads are
 //     contiguous); position p of sequence b holds token p;
-//   * grid (split, kv head, sequence): a workgroup takes 256 consecutive
-//     positions of one kv head for the G = Hq / Hkv query heads that share it
-//     (GQA), one key per thread, and writes its partial softmax state (max,
-//     sum of exponentials, weighted value sum) per query head;
+//   * grid (split, kv head, sequence) of one-wave workgroups: a wave takes
+//     32 consecutive positions (more, in steps of 32, only when the cache
+//     holds over 32768) of one kv head for the G = Hq / Hkv query heads that
+//     share it (GQA) and writes its partial softmax state (max, sum of
+//     exponentials, weighted value sum) per query head;
 //   * RoPE reads the cos / sin tables the reference builds (build_rope_cache,
 //     [max_positions][head_dim / 2] float32) at the token's position;
 //   * the new token's k / v are rotated, rounded to float16 and used directly
 //     by the workgroup whose range holds their position, which also stores
 //     them in the cache (no other workgroup reads that position);
-//   * only the workgroups whose range holds keys (positions 0 .. p) do any
-//     work; a second launch, one workgroup per (sequence, kv head), merges
-//     their partial states (max over the splits, rescaled sums) and writes the
+//   * only the waves whose range holds keys (positions 0 .. p) do any work;
+//     a second launch, one workgroup per (sequence, query head), merges their
+//     partial states (max over the splits, rescaled sums) and writes the
 //     output.
 #include <math.h>
 
@@ -118,9 +119,10 @@ int rms_norm_launch(const float* x, const float* w, float eps, float* y, uint16_
 // ---------------------------------------------------------------------------
 // decode attention
 // ---------------------------------------------------------------------------
-constexpr int kAttnChunk = 256;  // positions per workgroup
-constexpr int kMaxSplits = 512;  // splits per (sequence, kv head): max_positions <= 131072
-constexpr int kMaxGroup = 8;     // query heads per kv head (1, 2, 4 or 8)
+constexpr int kAttnKeys = 32;     // positions per wave and step
+constexpr int kMaxSplits = 1024;  // wave splits per (sequence, kv head)
+constexpr int kMaxGroup = 8;      // query heads per kv head (1, 2, 4 or 8)
+constexpr int kMaxPositions = 1 << 17;
 
 struct AttnArgs {
   const float* q;          // [B, Hq * D]
@@ -130,251 +132,296 @@ struct AttnArgs {
   uint16_t* vc;
   const int* positions;    // [B]
   void* out;               // [B, Hq * D] float32 or bfloat16
-  float* part;             // [B, Hkv, S, G, D + 2] partial softmax states
+  float* part;             // [B, Hkv, S, G, D + 4] partial softmax states: m, l, 0, 0, o[D]
   const float* cos_t;      // [P, D / 2] RoPE tables, NULL: no rotation
   const float* sin_t;
-  int hq, hkv, max_pos, splits;
+  int hq, hkv, max_pos;
+  int splits;              // waves per (sequence, kv head)
+  int steps;               // kAttnKeys-position steps per wave
   float scale;
   int out_bf16;
 };
 
+// The split geometry for a cache of max_pos positions: each wave takes
+// `steps` consecutive runs of kAttnKeys positions, at most kMaxSplits waves.
+struct AttnSplit {
+  int steps, splits;
+};
+inline AttnSplit attn_split(int64_t max_pos) {
+  const int64_t runs = (max_pos + kAttnKeys - 1) / kAttnKeys;
+  const int steps = (int)((runs + kMaxSplits - 1) / kMaxSplits);
+  return {steps, (int)((runs + steps - 1) / steps)};
+}
+
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
-// (x1, x2) -> (x1 c - x2 s, x2 c + x1 s), the reference's apply_rope pair (ops.py:82-92)
-__device__ __forceinline__ void rope_pair(const AttnArgs& a, int pos, int i, int half, float& x1, float& x2) {
-  if (!a.cos_t) return;
-  const float c = a.cos_t[(size_t)pos * half + i], s = a.sin_t[(size_t)pos * half + i];
-  const float r1 = x1 * c - x2 * s, r2 = x2 * c + x1 * s;
-  x1 = r1;
-  x2 = r2;
+// Sum over the lanes that share a lane index modulo LK (the key slots of a
+// wave), result in every lane.
+template <int LK>
+__device__ __forceinline__ float slot_sum(float v) {
+#pragma unroll
+  for (int m = LK; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+template <int LK>
+__device__ __forceinline__ float slot_max(float v) {
+#pragma unroll
+  for (int m = LK; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
 }
 
+__device__ __forceinline__ void f16x8_to_f32(const uint4 w, float (&f)[8]) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = f16_to_f32((uint16_t)(ws[e] & 0xFFFFu));
+    f[2 * e + 1] = f16_to_f32((uint16_t)(ws[e] >> 16));
+  }
+}
+
+// One wave per workgroup; grid (split, kv head, sequence).  The wave takes
+// positions [split * steps * 32, +steps * 32) of (sequence, kv head) for its G
+// query heads.  Lane mapping per 16-byte load: LK = D / 8 lanes per key (8
+// dimensions each), 64 / LK keys per load, NPW loads per lane cover 32 keys;
+// every key and value load of a step is issued before any math.  Scores are
+// summed over a key's LK lanes with DPP (every lane of the key holds it),
+// softmax statistics over the wave's keys with lane exchanges, and the value
+// sums are accumulated per lane over its key slot, rescaled across steps
+// (online softmax) and summed over the slots at the end.  No workgroup
+// barrier anywhere: a wave with no keys returns at once.
 template <int D, int G>
-__global__ __launch_bounds__(256) void decode_attention_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64) void decode_attention_kernel(AttnArgs a) {
   constexpr int HALF = D / 2;
-  constexpr int LK = D / 8;            // lanes per key: each holds 8 dimensions (one 16-byte load)
-  constexpr int KS = 256 / LK;         // keys per pass of the workgroup
-  constexpr int NP = kAttnChunk / KS;  // passes over the chunk
-  constexpr bool EARLY_V = G <= 4;     // value loads issued with the key loads (register budget)
-  __shared__ float qs[G][D];           // rotated queries of the group
-  __shared__ float kn[D];              // the new token's rotated key (float16-rounded)
+  constexpr int LK = D / 8;
+  constexpr int KPL = 64 / LK;
+  constexpr int NPW = kAttnKeys / KPL;
+  __shared__ float qs[G][D];  // rotated queries of the group
+  __shared__ float kn[D];     // the new token's rotated key (float16-rounded)
   __shared__ float vn[D];
-  __shared__ float ps[G][kAttnChunk];
-  __shared__ float red[G][4];
-  __shared__ float accs[KS][D];        // one query head's value sums per key slot
 
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int t = threadIdx.x;
+  const int lane = threadIdx.x;
   const int pos = a.positions[b];
   const bool valid = pos >= 0 && pos < a.max_pos;  // else no cache access; the output is NaN
   const int n_keys = valid ? pos + 1 : 0;
-  const int used = (n_keys + kAttnChunk - 1) / kAttnChunk;  // workgroups holding keys
-  const int j0 = split * kAttnChunk;
-  const int jn = min(kAttnChunk, n_keys - j0);  // keys of this workgroup (<= 0: none)
-  if (split >= used || jn <= 0) return;  // no keys
+  const int span = kAttnKeys * a.steps;
+  const int j0 = split * span;
+  if (j0 >= n_keys) return;
+  const int jend = min(j0 + span, n_keys);
   const size_t head = ((size_t)b * a.hkv + h) * (size_t)a.max_pos * D;
-  float* part = a.part + (((size_t)b * a.hkv + h) * a.splits + split) * G * (D + 2);
-  // thread t: dimensions 8 * (t % LK) .. + 7 of key slot t / LK of each pass
-  const int dl = t % LK, slot = t / LK;
+  const int dl = lane % LK, slot = lane / LK;
 
-  if (jn > 0) {
-    // every key (and value) load of the chunk first: their addresses need only the position
-    uint4 kw[NP], vw[EARLY_V ? NP : 1];
+  // the query (and new key / value) elements and RoPE factors first: they
+  // come from L2 and are rotated while the cache loads are in flight
+  constexpr int QE = (G * HALF + 63) / 64;  // (g, i) pairs per lane
+  float q1[QE], q2[QE], qc[QE], qn[QE];
+  const float* qb = a.q + (size_t)b * a.hq * D + (size_t)h * G * D;
 #pragma unroll
-    for (int r = 0; r < NP; ++r) {
-      const int jj = slot + KS * r;
-      const size_t at = head + (size_t)(j0 + (jj < jn ? jj : 0)) * D + 8 * dl;
-      kw[r] = *reinterpret_cast<const uint4*>(a.kc + at);
-      if constexpr (EARLY_V) vw[r] = *reinterpret_cast<const uint4*>(a.vc + at);
-    }
-    // queries (and, for the workgroup holding the new position, k / v), rotated
-    for (int e = t; e < G * HALF; e += 256) {
+  for (int u = 0; u < QE; ++u) {
+    const int e = min(lane + 64 * u, G * HALF - 1);
+    const int g = e / HALF, i = e - g * HALF;
+    q1[u] = qb[g * D + i];
+    q2[u] = qb[g * D + i + HALF];
+    qc[u] = a.cos_t ? a.cos_t[(size_t)pos * HALF + i] : 1.f;
+    qn[u] = a.cos_t ? a.sin_t[(size_t)pos * HALF + i] : 0.f;
+  }
+  const bool owner = pos >= j0 && pos < jend;
+  const int io = min(lane, HALF - 1);
+  float k1 = 0.f, k2 = 0.f, v1 = 0.f, v2 = 0.f;
+  if (owner) {
+    const float* kp = a.k + ((size_t)b * a.hkv + h) * D;
+    const float* vp = a.v + ((size_t)b * a.hkv + h) * D;
+    k1 = kp[io];
+    k2 = kp[io + HALF];
+    v1 = vp[io];
+    v2 = vp[io + HALF];
+  }
+  uint4 kw[NPW], vw[NPW];
+#pragma unroll
+  for (int r = 0; r < NPW; ++r) {
+    const int jj = slot + KPL * r;
+    const size_t at = head + (size_t)(j0 + (j0 + jj < jend ? jj : 0)) * D + 8 * dl;
+    kw[r] = *reinterpret_cast<const uint4*>(a.kc + at);
+    vw[r] = *reinterpret_cast<const uint4*>(a.vc + at);
+  }
+#pragma unroll
+  for (int u = 0; u < QE; ++u) {
+    const int e = lane + 64 * u;
+    if (e < G * HALF) {
       const int g = e / HALF, i = e - g * HALF;
-      const float* qp = a.q + (size_t)b * a.hq * D + (size_t)(h * G + g) * D;
-      float x1 = qp[i], x2 = qp[i + HALF];
-      rope_pair(a, pos, i, HALF, x1, x2);
-      qs[g][i] = x1;
-      qs[g][i + HALF] = x2;
+      qs[g][i] = q1[u] * qc[u] - q2[u] * qn[u];
+      qs[g][i + HALF] = q2[u] * qc[u] + q1[u] * qn[u];
     }
-    const bool owner = pos >= j0 && pos < j0 + kAttnChunk;
-    if (owner) {
-      for (int i = t; i < HALF; i += 256) {
-        const float* kp = a.k + ((size_t)b * a.hkv + h) * D;
-        const float* vp = a.v + ((size_t)b * a.hkv + h) * D;
-        float x1 = kp[i], x2 = kp[i + HALF];
-        rope_pair(a, pos, i, HALF, x1, x2);
-        const uint16_t k1 = f32_to_f16(x1), k2 = f32_to_f16(x2);
-        const uint16_t v1 = f32_to_f16(vp[i]), v2 = f32_to_f16(vp[i + HALF]);
-        kn[i] = f16_to_f32(k1);
-        kn[i + HALF] = f16_to_f32(k2);
-        vn[i] = f16_to_f32(v1);
-        vn[i + HALF] = f16_to_f32(v2);
-        a.kc[head + (size_t)pos * D + i] = k1;
-        a.kc[head + (size_t)pos * D + i + HALF] = k2;
-        a.vc[head + (size_t)pos * D + i] = v1;
-        a.vc[head + (size_t)pos * D + i + HALF] = v2;
-      }
-    }
-    __syncthreads();
+  }
+  if (owner && lane < HALF) {
+    // (x1, x2) -> (x1 c - x2 s, x2 c + x1 s), the reference's apply_rope pair
+    // (ops.py:82-92), then the float16 cache dtype
+    const float c = qc[0], sn = qn[0];  // lane < HALF: pair i = lane, the same factors as q's
+    const uint16_t kh1 = f32_to_f16(k1 * c - k2 * sn), kh2 = f32_to_f16(k2 * c + k1 * sn);
+    const uint16_t vh1 = f32_to_f16(v1), vh2 = f32_to_f16(v2);
+    kn[lane] = f16_to_f32(kh1);
+    kn[lane + HALF] = f16_to_f32(kh2);
+    vn[lane] = f16_to_f32(vh1);
+    vn[lane + HALF] = f16_to_f32(vh2);
+    a.kc[head + (size_t)pos * D + lane] = kh1;
+    a.kc[head + (size_t)pos * D + lane + HALF] = kh2;
+    a.vc[head + (size_t)pos * D + lane] = vh1;
+    a.vc[head + (size_t)pos * D + lane + HALF] = vh2;
+  }
+  __syncthreads();  // one wave: orders the LDS writes before the reads
+  float qr[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qr[g][e] = qs[g][8 * dl + e];
 
-    float qr[G][8];
+  float m[G], l[G], o[G][8];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qr[g][e] = qs[g][8 * dl + e];
-
-    // scores (the new position's key comes from LDS)
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
+  }
+  for (int js = j0;;) {
+    const int jn = min(kAttnKeys, jend - js);  // keys of this step
+    float s[G][NPW];
 #pragma unroll
-    for (int r = 0; r < NP; ++r) {
-      const int jj = slot + KS * r;
+    for (int r = 0; r < NPW; ++r) {
+      const int jj = slot + KPL * r;
       float kv[8];
-      if (j0 + jj == pos) {
+      if (js + jj == pos) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) kv[e] = kn[8 * dl + e];
       } else {
-        const uint32_t ws[4] = {kw[r].x, kw[r].y, kw[r].z, kw[r].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          kv[2 * e] = f16_to_f32((uint16_t)(ws[e] & 0xFFFFu));
-          kv[2 * e + 1] = f16_to_f32((uint16_t)(ws[e] >> 16));
-        }
+        f16x8_to_f32(kw[r], kv);
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float dot = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) dot = fmaf(qr[g][e], kv[e], dot);
-        dot = group_sum_dpp<LK>(dot);  // the key's LK lanes
-        if (dl == 0) ps[g][jj] = jj < jn ? dot * a.scale : -INFINITY;
+        dot = group_sum_dpp<LK>(dot);
+        s[g][r] = jj < jn ? dot * a.scale : -INFINITY;
       }
     }
-    if constexpr (!EARLY_V) {
 #pragma unroll
-      for (int r = 0; r < NP; ++r) {
-        const int jj = slot + KS * r;
-        kw[r] = *reinterpret_cast<const uint4*>(a.vc + head + (size_t)(j0 + (jj < jn ? jj : 0)) * D + 8 * dl);
+    for (int g = 0; g < G; ++g) {
+      float mx = s[g][0];
+#pragma unroll
+      for (int r = 1; r < NPW; ++r) mx = fmaxf(mx, s[g][r]);
+      const float mn = fmaxf(m[g], slot_max<LK>(mx));
+      const float corr = expf(m[g] - mn);  // 0 on the first step
+      float ps = 0.f;
+#pragma unroll
+      for (int r = 0; r < NPW; ++r) {
+        s[g][r] = expf(s[g][r] - mn);
+        ps += s[g][r];
       }
+      l[g] = l[g] * corr + slot_sum<LK>(ps);  // one lane per key slot in each exchange
+      m[g] = mn;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] *= corr;
     }
-    __syncthreads();
-
-    // max and sum of exponentials per query head (thread t < chunk <-> key t)
-    float m[G], l[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float v = wave_max_dpp(t < kAttnChunk ? ps[g][t] : -INFINITY);
-      if ((t & 63) == 0) red[g][t >> 6] = v;
-    }
-    __syncthreads();
-    float pv[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      m[g] = fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3]));
-      pv[g] = t < jn ? expf(ps[g][t] - m[g]) : 0.f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      if (t < kAttnChunk) ps[g][t] = pv[g];
-      const float v = wave_sum_dpp(pv[g]);
-      if ((t & 63) == 0) red[g][t >> 6] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g) l[g] = red[g][0] + red[g][1] + red[g][2] + red[g][3];
-
-    // weighted value sums, the same lane mapping
-    float o[G][8];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
-#pragma unroll
-    for (int r = 0; r < NP; ++r) {
-      const int jj = slot + KS * r;
-      const uint4 w = EARLY_V ? vw[EARLY_V ? r : 0] : kw[r];
+    for (int r = 0; r < NPW; ++r) {
+      const int jj = slot + KPL * r;
       float vv[8];
-      if (j0 + jj == pos) {
+      if (js + jj == pos) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) vv[e] = vn[8 * dl + e];
       } else {
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          vv[2 * e] = f16_to_f32((uint16_t)(ws[e] & 0xFFFFu));
-          vv[2 * e + 1] = f16_to_f32((uint16_t)(ws[e] >> 16));
-        }
+        f16x8_to_f32(vw[r], vv);
       }
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float p = jj < jn ? ps[g][jj] : 0.f;
+      for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] = fmaf(p, vv[e], o[g][e]);
-      }
+        for (int e = 0; e < 8; ++e) o[g][e] = fmaf(s[g][r], vv[e], o[g][e]);
     }
-    // sum over the KS key slots through LDS, one query head at a time
+    js += kAttnKeys;
+    if (js >= jend) break;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) accs[slot][8 * dl + e] = o[g][e];
-      __syncthreads();
-      if (t < D) {
-        float v = 0.f;
-#pragma unroll
-        for (int k2 = 0; k2 < KS; ++k2) v += accs[k2][t];
-        part[g * (D + 2) + 2 + t] = v;
-      }
-      __syncthreads();
+    for (int r = 0; r < NPW; ++r) {
+      const int jj = slot + KPL * r;
+      const size_t at = head + (size_t)(js + (js + jj < jend ? jj : 0)) * D + 8 * dl;
+      kw[r] = *reinterpret_cast<const uint4*>(a.kc + at);
+      vw[r] = *reinterpret_cast<const uint4*>(a.vc + at);
     }
-    if (t < G) {
-      part[t * (D + 2)] = m[t];
-      part[t * (D + 2) + 1] = l[t];
+  }
+  // value sums over the key slots; slot 0's lanes write the partial state
+  float* part = a.part + (((size_t)b * a.hkv + h) * a.splits + split) * G * (D + 4);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = slot_sum<LK>(o[g][e]);
+    if (slot == 0) {
+      float4* dst = reinterpret_cast<float4*>(part + g * (D + 4) + 4 + 8 * dl);
+      dst[0] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+      dst[1] = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
+      if (dl == 0) *reinterpret_cast<float4*>(part + g * (D + 4)) = make_float4(m[g], l[g], 0.f, 0.f);
     }
   }
 }
 
-// Merges the partial states of the `used` workgroups of (sequence b, kv head h)
-// (a second launch: the kernel boundary makes the partials visible).
+// Merges the partial states of the `used` waves of one query head of
+// sequence b (a second launch: the kernel boundary makes the partials
+// visible).  Grid (query head, sequence).  Thread t takes dimensions
+// 4 (t % (D / 4)) .. + 3 of the splits s = t / (D / 4) (mod the phases) and
+// merges them as it loads them (running max, rescaled sums), so every load
+// of the launch is issued at once; the phases meet in LDS.
 template <int D, int G>
 __global__ __launch_bounds__(256) void decode_merge_kernel(AttnArgs a) {
-  __shared__ float ms[kMaxSplits][G];  // split maxima, then their weights exp(m_s - M)
-  __shared__ float ls[kMaxSplits][G];
-  __shared__ float mg[G], dg[G];
-  const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  constexpr int TQ = D / 4;      // threads per split row (float4 each)
+  constexpr int NPH = 256 / TQ;  // split phases
+  __shared__ float pm[NPH], pl[NPH];
+  __shared__ float4 acc[NPH][TQ];
+  const int qh = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int h = qh / G, g = qh - h * G;
   const int pos = a.positions[b];
   const bool valid = pos >= 0 && pos < a.max_pos;
-  const int used = valid ? (pos + kAttnChunk) / kAttnChunk : 0;
-  const float* base = a.part + ((size_t)b * a.hkv + h) * a.splits * G * (D + 2);
-  for (int i = t; i < used * G; i += 256) {
-    const int sp = i / G, g = i - sp * G;
-    ms[sp][g] = base[(sp * G + g) * (D + 2)];
-    ls[sp][g] = base[(sp * G + g) * (D + 2) + 1];
+  const int span = kAttnKeys * a.steps;
+  const int used = valid ? (pos + span) / span : 0;
+  const size_t stride = (size_t)G * (D + 4);
+  const float* base = a.part + (((size_t)b * a.hkv + h) * a.splits * G + g) * (D + 4);
+  const int dq = t % TQ, ph = t / TQ;
+  float M = -INFINITY, L = 0.f;
+  float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+  for (int sp = ph; sp < used; sp += NPH) {
+    const float* p = base + sp * stride;
+    const float2 ml = *reinterpret_cast<const float2*>(p);
+    const float4 o4 = *reinterpret_cast<const float4*>(p + 4 + 4 * dq);
+    const float mn = fmaxf(M, ml.x);
+    const float co = expf(M - mn), cn = expf(ml.x - mn);
+    L = fmaf(L, co, ml.y * cn);
+    s4.x = fmaf(s4.x, co, o4.x * cn);
+    s4.y = fmaf(s4.y, co, o4.y * cn);
+    s4.z = fmaf(s4.z, co, o4.z * cn);
+    s4.w = fmaf(s4.w, co, o4.w * cn);
+    M = mn;
   }
-  __syncthreads();
-  if (t < G) {
-    float mx = -INFINITY;
-    for (int sp = 0; sp < used; ++sp) mx = fmaxf(mx, ms[sp][t]);
-    mg[t] = mx;
+  if (dq == 0) {
+    pm[ph] = M;
+    pl[ph] = L;
   }
+  acc[ph][dq] = s4;
   __syncthreads();
-  for (int i = t; i < used * G; i += 256) {
-    const int sp = i / G, g = i - sp * G;
-    ms[sp][g] = expf(ms[sp][g] - mg[g]);
-  }
-  __syncthreads();
-  if (t < G) {
-    float den = 0.f;
-    for (int sp = 0; sp < used; ++sp) den = fmaf(ls[sp][t], ms[sp][t], den);
-    dg[t] = den;
-  }
-  __syncthreads();
-  for (int e = t; e < G * D; e += 256) {
-    const int g = e / D, d = e - g * D;
-    float num = 0.f;
-#pragma unroll 8
-    for (int sp = 0; sp < used; ++sp) num = fmaf(base[(sp * G + g) * (D + 2) + 2 + d], ms[sp][g], num);
-    const float r = valid ? num / dg[g] : __builtin_nanf("");
-    const size_t at = (size_t)b * a.hq * D + (size_t)(h * G + g) * D + d;
+  if (t < D) {
+    float mg = pm[0];
+#pragma unroll
+    for (int p = 1; p < NPH; ++p) mg = fmaxf(mg, pm[p]);
+    const int q4 = t / 4, c = t & 3;
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int p = 0; p < NPH; ++p) {
+      const float w = pm[p] == -INFINITY ? 0.f : expf(pm[p] - mg);  // a phase without splits weighs 0
+      const float4 v = acc[p][q4];
+      num = fmaf(c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w, w, num);
+      den = fmaf(pl[p], w, den);
+    }
+    const float r = valid ? num / den : __builtin_nanf("");
+    const size_t at = (size_t)b * a.hq * D + (size_t)qh * D + t;
     if (a.out_bf16)
       static_cast<uint16_t*>(a.out)[at] = f32_to_bf16_bits(r);
     else
@@ -383,8 +430,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(AttnArgs a) {
 }
 
 size_t decode_attention_ws(int64_t batch, int hq, int hkv, int head_dim, int64_t max_pos) {
-  const int64_t splits = (max_pos + kAttnChunk - 1) / kAttnChunk;
-  return (size_t)batch * hkv * splits * (hq / hkv) * (head_dim + 2) * sizeof(float);
+  const AttnSplit sp = attn_split(max_pos);
+  return (size_t)batch * hkv * sp.splits * (hq / hkv) * (head_dim + 4) * sizeof(float);
 }
 
 int decode_attention_launch(const float* q, const float* k, const float* v, uint16_t* kc, uint16_t* vc,
@@ -403,16 +450,18 @@ int decode_attention_launch(const float* q, const float* k, const float* v, uint
   a.hq = hq;
   a.hkv = hkv;
   a.max_pos = (int)max_pos;
-  a.splits = (int)((max_pos + kAttnChunk - 1) / kAttnChunk);
+  const AttnSplit sp = attn_split(max_pos);
+  a.splits = sp.splits;
+  a.steps = sp.steps;
   a.cos_t = cos_t;
   a.sin_t = sin_t;
   a.scale = (float)(1.0 / sqrt((double)head_dim));
   a.out_bf16 = out_bf16;
   const dim3 grid((unsigned)a.splits, (unsigned)hkv, (unsigned)batch);
   const int g = hq / hkv;
-  const dim3 mgrid((unsigned)hkv, (unsigned)batch);
+  const dim3 mgrid((unsigned)hq, (unsigned)batch);
 #define DRACO_ATTN_LAUNCH(D_, G_)                                                                \
-  hipLaunchKernelGGL((decode_attention_kernel<D_, G_>), grid, dim3(256), 0, s, a);              \
+  hipLaunchKernelGGL((decode_attention_kernel<D_, G_>), grid, dim3(64), 0, s, a);               \
   if (int rc = check_launch("decode_attention")) return rc;                                    \
   hipLaunchKernelGGL((decode_merge_kernel<D_, G_>), mgrid, dim3(256), 0, s, a)
   if (head_dim == 128) {
@@ -478,7 +527,7 @@ int draco_gguf_decode_attention(const float* q, const float* k, const float* v, 
   if (head_dim != 64 && head_dim != 128)
     return set_error(DRACO_EINVAL_SHAPE, "decode attention takes head_dim 64 or 128, got %d", head_dim);
   if (max_positions < 1 || max_positions * head_dim * (int64_t)n_kv_heads * batch > ((int64_t)1 << 40) ||
-      max_positions > (int64_t)kMaxSplits * kAttnChunk)
+      max_positions > kMaxPositions)
     return set_error(DRACO_EINVAL_SHAPE, "invalid max_positions %lld", (long long)max_positions);
   if ((rope_cos == nullptr) != (rope_sin == nullptr))
     return set_error(DRACO_EINVAL_ARG, "rope_cos and rope_sin must both be given or both be NULL");

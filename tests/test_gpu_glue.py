@@ -71,7 +71,7 @@ def _attention_case(b, hq, hkv, d, max_pos, positions, theta, rope, seed, out_dt
     return got
 
 
-@pytest.mark.parametrize("positions", [[0], [5, 700], [255, 256], [511, 1023]])
+@pytest.mark.parametrize("positions", [[0], [5, 700], [255, 256], [511, 1023], [31, 32, 33, 95]])
 def test_decode_attention_llama_heads(positions):
     print(f"decode attention positions {positions}", flush=True)
     _attention_case(len(positions), 32, 8, 128, 1024, positions, 500000.0, True, seed=sum(positions) + 1)
@@ -81,6 +81,13 @@ def test_decode_attention_llama_heads(positions):
 def test_decode_attention_shapes(hq, hkv, d, rope):
     print(f"decode attention hq={hq} hkv={hkv} d={d} rope={rope}", flush=True)
     _attention_case(3, hq, hkv, d, 600, [0, 299, 599], 10000.0, rope, seed=hq + d)
+
+
+def test_decode_attention_long_cache_multi_step_waves():
+    """A cache of 40000 positions: each wave walks two 32-position steps
+    (online rescaling inside the wave) and 625 waves meet in the merge."""
+    print("decode attention max_pos 40000", flush=True)
+    _attention_case(2, 8, 2, 64, 40000, [39999, 12345], 500000.0, True, seed=40)
 
 
 def test_decode_attention_bf16_out_and_invalid_position():

@@ -234,15 +234,18 @@ __device__ __forceinline__ void x1_fetch_x_rmsnorm(const float* __restrict__ h, 
       }
     }
   }
-  const float denom = sqrtf(block_sum_256(ss, red) / (float)k + eps);
+  // x * (1 / r) in place of the reference's x / r: within one float32 ulp,
+  // below the bfloat16 rounding that follows, and one division per thread
+  // instead of sixteen
+  const float inv = 1.f / sqrtf(block_sum_256(ss, red) / (float)k + eps);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     uint32_t pk[4];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const float4 a = v[2 * j + q], b = g[2 * j + q];
-      pk[2 * q] = f32_to_bf16_rne(a.x / denom * b.x) | ((uint32_t)f32_to_bf16_rne(a.y / denom * b.y) << 16);
-      pk[2 * q + 1] = f32_to_bf16_rne(a.z / denom * b.z) | ((uint32_t)f32_to_bf16_rne(a.w / denom * b.w) << 16);
+      pk[2 * q] = f32_to_bf16_rne(a.x * inv * b.x) | ((uint32_t)f32_to_bf16_rne(a.y * inv * b.y) << 16);
+      pk[2 * q + 1] = f32_to_bf16_rne(a.z * inv * b.z) | ((uint32_t)f32_to_bf16_rne(a.w * inv * b.w) << 16);
     }
     xr[j] = uint4{pk[0], pk[1], pk[2], pk[3]};
     const int c = (int)threadIdx.x + 256 * j;
@@ -586,6 +589,80 @@ static int launch_x1p(const StreamJob& job, int blocks_per_cu, hipStream_t s) {
   return check_launch("gemv_x1p");
 }
 
+// Persistent form for rows of S steps (4096 < K <= 4096 S; the down
+// projection, K = 14336, has S = 4): the same row walk as above over items
+// (row, step), PF items ahead in flight (one: two was measured slower).  A step's activations come from the
+// LDS image at every item (64 bf16 and the group sums per lane), the unit
+// dots of a row accumulate per lane and meet in one wave reduction when the
+// row's last step is done.
+template <int QT, bool DL, int MODE, int S, int PF>
+__global__ __launch_bounds__(256) void gemv_x1s_kernel(StreamJob job) {
+  static_assert(MODE != kSwiGLU, "one matrix per row");
+  constexpr int NB = PF + 1;  // item ring: the current item and PF in flight
+  extern __shared__ uint4 x1_smem[];
+  const int lane = threadIdx.x & 63;
+  const X1Rows<MODE> rows(job);
+  const int nrow = rows.nrow;
+  const int k = job.k;
+  const int units = k >> 6;
+
+  // 1. activations (2 S 16-byte chunks per thread), then the first item
+  uint4 xr[2 * S];
+  x1_fetch_x<2 * S>(job.x, k, xr);
+  X1Raw<QT> buf[NB];
+#pragma unroll
+  for (int p = 0; p < PF; ++p) {
+    const int ip = p / S, sp = p - ip * S;
+    const int up = lane + 64 * sp;
+    buf[p] = x1_load<QT, DL>(rows.buf(job, ip, 0), up < units ? up : units - 1);
+  }
+
+  // 2. the LDS image and group sums
+  x1_stage_regs<QT, 2 * S>(x1_smem, xr, k);
+  if (nrow == 0) return;
+  const X1Lane lc = x1_lane<QT>(lane);
+
+  // 3. items t = (row t / S, step t % S), NB per iteration so the ring
+  // index is static
+  const int total = nrow * S;
+  float res = 0.f, acc = 0.f;
+  for (int t0 = 0; t0 < total; t0 += NB) {
+#pragma unroll
+    for (int p = 0; p < NB; ++p) {
+      const int t = t0 + p;
+      const int in = (t + PF) / S, sn = (t + PF) - in * S;
+      const int un = lane + 64 * sn;
+      buf[(p + PF) % NB] = x1_load<QT, DL>(rows.buf(job, in, 0), un < units ? un : units - 1);
+      __builtin_amdgcn_sched_barrier(0);  // keep the load ahead of the math
+      if (t < total) {
+        const int i = t / S, s = t - i * S;
+        X1Act xa;
+        x1_read_lds<QT>(x1_smem, k, s, lane, lane + 64 * s < units, xa);
+        acc += x1_unit_dot<QT>(buf[p], lc, xa);
+        if (s == S - 1) {
+          const float v = wave_sum_dpp(acc);
+          acc = 0.f;
+          res = (lane == (i & 63)) ? v : res;
+          if ((i & 63) == 63) rows.flush(job, i - 63, 64, res);
+        }
+      }
+    }
+  }
+  if (nrow & 63) rows.flush(job, nrow & ~63, nrow & 63, res);
+}
+
+template <int QT, bool DL, int MODE, int S, int PF = 1>
+static int launch_x1s(const StreamJob& job, int blocks_per_cu, hipStream_t s) {
+  const int steps = ((job.k >> 6) + 63) >> 6;
+  if (steps != S || job.k % 256 != 0) return set_error(DRACO_EINVAL_SHAPE, "GEMV row of %d steps, kernel takes %d", steps, S);
+  const size_t lds = x1p_lds_bytes(QT, job.k);
+  if (lds > 64 * 1024) return set_error(DRACO_EINVAL_SHAPE, "activation image needs %zu bytes of LDS", lds);
+  const int need = (job.rows + 3) / 4;
+  const int blocks = std::max(1, std::min(need, device_cus() * blocks_per_cu));
+  hipLaunchKernelGGL((gemv_x1s_kernel<QT, DL, MODE, S, PF>), dim3(blocks), dim3(256), lds, s, job);
+  return check_launch("gemv_x1s");
+}
+
 // ---------------------------------------------------------------------------
 // Q4_K persistent form with 32-weight units (the streaming kernel's unit: one
 // 16-byte qs load per lane, eight lanes per super-block, so a wave's qs load
@@ -791,6 +868,22 @@ static int gemv_dispatch_mode(int qtype, bool d_last, const StreamJob& job, bool
   // streaming kernel from 8 rows on; at 4 rows they tie or the latter wins)
   if (job.m >= 8 && mfma_gemv_ok(qtype, job, xbf16)) return gemv_mfma_dispatch<MODE>(qtype, d_last, job, xbf16, s);
   if constexpr (MODE != kSwiGLU) {
+    // rows of 2..4 steps (K <= 16384, the down projection): the persistent
+    // multi-step form
+    const int steps = ((job.k >> 6) + 63) >> 6;
+    if (x1 && steps >= 2 && steps <= 4 && job.k % 256 == 0 && x1p_lds_bytes(qtype, job.k) <= 64 * 1024) {
+      constexpr int bpc = 3;
+#define DRACO_X1S(S_)                                                                      \
+  if (steps == S_) {                                                                       \
+    if (qtype == kQ4_K) return launch_x1s<kQ4_K, false, MODE, S_>(job, bpc, s);             \
+    return d_last ? launch_x1s<kQ6_K, true, MODE, S_>(job, bpc, s)                         \
+                  : launch_x1s<kQ6_K, false, MODE, S_>(job, bpc, s);                       \
+  }
+      DRACO_X1S(2)
+      DRACO_X1S(3)
+      DRACO_X1S(4)
+#undef DRACO_X1S
+    }
     if (x1 && x1_lds_bytes(qtype, job.k) <= 64 * 1024) {
       if (qtype == kQ4_K) return launch_x1<kQ4_K, false, MODE, 2, 1, false, true>(job, s);
       return d_last ? launch_x1<kQ6_K, true, MODE, 2, 1, false, true>(job, s)

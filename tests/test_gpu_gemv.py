@@ -81,3 +81,22 @@ def test_gemv_batched_decode_equals_sequential():
     for i in range(8):
         yi = gguf_gemv(x[i:i + 1].contiguous(), q, Q4_K, (1024, 4096))
         assert torch.allclose(yb[i], yi[0], rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K, Q6_K | 0x100])
+def test_gemv_single_token_multi_step_rows(qtype):
+    """One bf16 token over rows of 2, 3 and 4 steps of 64 units (K = 8192,
+    11008, 14336, 16384) and row counts that leave waves empty or partly
+    filled: the persistent multi-step form, plain and residual modes."""
+    from dracort_amd.kernels import gguf_gemv_residual
+    for n, k in ((300, 8192), (77, 11008), (4096, 14336), (5, 16384)):
+        print(f"gemv x1s {qtype:#x} [{n},{k}]", flush=True)
+        y, ref = _run(qtype, n, k, 1, torch.bfloat16, seed=n + k)
+        check_close(y, ref, f"{qtype:#x} [{n},{k}]")
+    blocks, w = quantized(qtype, 640, 11008, 3)
+    x = activations(1, 11008, 3, torch.bfloat16)
+    resid = torch.from_numpy(np.random.default_rng(3).standard_normal((1, 640)).astype(np.float32))
+    ref = resid.numpy().astype(np.float64) + matmul_ref.linear_ref(x.float().numpy(), w)
+    r = resid.cuda()
+    gguf_gemv_residual(x.cuda(), torch.from_numpy(blocks).cuda(), qtype, (640, 11008), r)
+    check_close(r.cpu().numpy(), ref, f"{qtype:#x} residual")

@@ -145,8 +145,6 @@ __device__ __forceinline__ int x1_slot_of_chunk(int c) {  // natural chunk (8 bf
   return j * 64 + u;
 }
 
-inline size_t tile_x_lds_bytes_q4k(int k) { return (size_t)k * 2 + (size_t)(k / 32) * 2 * sizeof(float); }
-
 __host__ __device__ inline size_t x1_lds_bytes(int qtype, int k) {
   const int steps = ((k >> 6) + 63) >> 6;
   const int g = qtype == kQ4_K ? 2 : 4;
@@ -661,151 +659,6 @@ static int launch_x1s(const StreamJob& job, int blocks_per_cu, hipStream_t s) {
   const int blocks = std::max(1, std::min(need, device_cus() * blocks_per_cu));
   hipLaunchKernelGGL((gemv_x1s_kernel<QT, DL, MODE, S, PF>), dim3(blocks), dim3(256), lds, s, job);
   return check_launch("gemv_x1s");
-}
-
-// ---------------------------------------------------------------------------
-// Q4_K persistent form with 32-weight units (the streaming kernel's unit: one
-// 16-byte qs load per lane, eight lanes per super-block, so a wave's qs load
-// covers 1 KB of 1152 consecutive bytes, plus the 16-byte block head).  This
-// load pattern was measured to stream faster than the 64-weight units (6.2 vs
-// 5.4 TB/s on a 302 MB weight with the math switched off).  Rows of K = 2048
-// or 4096 (S = K / 2048 steps of 64 units); the lane's activations of both
-// steps live in registers (the lane-permuted LDS image of the streaming
-// kernel, read once) and the next PF rows' blocks are in flight.
-// ---------------------------------------------------------------------------
-struct X2Act {
-  uint32_t w[2][16];  // [step][32 bf16 of the lane's unit]
-  float xs[2][2];     // [step][group] activation sums
-};
-
-// sum_i w_i x_i over one 32-weight Q4_K unit (groups of 16: low nibbles =
-// sub-block j0, high nibbles = j0 + 1, j0 = 2 * ((u & 7) >> 1)).
-__device__ __forceinline__ float x2_unit_dot(const Raw<kQ4_K>& r, const X1Lane& c, const uint32_t* xw,
-                                             const float* xs) {
-  const float d = f16_bits_to_f32(r.head.x), dmin = f16_bits_to_f32(r.head.x >> 16);
-  const uint32_t s0 = r.head.y, s1 = r.head.z, s2 = r.head.w;
-  const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, m_lo = s1 & 0x3F3F3F3Fu;
-  const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
-  const uint32_t m_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
-  const uint32_t scw = ((sc_hi & c.hi_mask) | (sc_lo & ~c.hi_mask)) >> c.sh;
-  const uint32_t mw = ((m_hi & c.hi_mask) | (m_lo & ~c.hi_mask)) >> c.sh;
-  const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
-  float out = 0.f;
-#pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    float dot = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t cw = g == 0 ? nib_lo(q[i]) : nib_hi(q[i]);
-      dot = dot2bf(code_pair_lo(cw), xw[8 * g + 2 * i], dot);
-      dot = dot2bf(code_pair_hi(cw), xw[8 * g + 2 * i + 1], dot);
-    }
-    out = fmaf(d * ubyte_f(scw, g), fmaf(-kCodeBias, xs[g], dot), out);
-    out = fmaf(-(dmin * ubyte_f(mw, g)), xs[g], out);
-  }
-  return out;
-}
-
-template <int MODE, int S, int PF>
-__global__ __launch_bounds__(256) void gemv_x2p_kernel(StreamJob job) {
-  constexpr int NR = MODE == kSwiGLU ? 2 : 1;
-  constexpr int STEP_BYTES = StepGeom<kQ4_K>::STEP_BYTES;  // 1152
-  extern __shared__ uint4 x2_smem[];
-  const int lane = threadIdx.x & 63;
-  const int W = gridDim.x * 4;
-  const int w = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int k = job.k;
-  const uint8_t* xb = static_cast<const uint8_t*>(job.x);
-  auto xrow = [&](int) { return (const void*)xb; };
-  stage_x_lds_perm<kQ4_K, 1, true>(x2_smem, 1, k, xrow);
-  float* xsum = reinterpret_cast<float*>(x2_smem + k * 2 / 16);
-  stage_group_sums_perm<kQ4_K, 1, true>(x2_smem, xsum, 1, k);
-  const int nrow = job.rows > w ? (job.rows - w + W - 1) / W : 0;
-  if (nrow == 0) return;
-
-  // the lane's activations: unit lane of each step (chunks c * 64 + lane of the step's image)
-  X2Act xa;
-#pragma unroll
-  for (int st = 0; st < S; ++st) {
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      const uint4 v = x2_smem[st * 256 + cc * 64 + lane];
-      xa.w[st][4 * cc] = v.x; xa.w[st][4 * cc + 1] = v.y; xa.w[st][4 * cc + 2] = v.z; xa.w[st][4 * cc + 3] = v.w;
-    }
-    const float2 sv = *reinterpret_cast<const float2*>(xsum + ((size_t)st * 64 + lane) * 2);
-    xa.xs[st][0] = sv.x;
-    xa.xs[st][1] = sv.y;
-  }
-  X1Lane lc;
-  lc.hi_mask = (lane & 7) >= 4 ? 0xFFFFFFFFu : 0u;
-  lc.sh = 16u * ((lane >> 1) & 1);
-
-  auto rowbuf = [&](int i, int q) {
-    int mat = 0, lrow = w + i * W;
-    if constexpr (MODE == kPlain) row_of(job, lrow, mat, lrow);
-    const int m = NR == 2 ? q : mat;
-    BufferLoader b;
-    b.rsrc = make_rsrc(job.w[m], (uint32_t)((int64_t)job.n[m] * job.row_bytes));
-    b.soff = (int)((int64_t)lrow * job.row_bytes);
-    return b;
-  };
-  auto load_row = [&](Raw<kQ4_K>(&dst)[NR][S], int i) {
-#pragma unroll
-    for (int q = 0; q < NR; ++q) {
-      BufferLoader b = rowbuf(i, q);
-#pragma unroll
-      for (int st = 0; st < S; ++st) {
-        BufferLoader bs = b;
-        bs.soff += st * STEP_BYTES;
-        dst[q][st] = load_unit_l<kQ4_K, false>(bs, 0, lane);
-      }
-    }
-  };
-  Raw<kQ4_K> buf[PF][NR][S];
-#pragma unroll
-  for (int p = 0; p < PF; ++p) load_row(buf[p], min(p, nrow - 1));
-
-  for (int i0 = 0; i0 < nrow; i0 += PF) {
-#pragma unroll
-    for (int p = 0; p < PF; ++p) {
-      const int i = i0 + p;
-      if (i < nrow) {
-        float v[NR];
-#pragma unroll
-        for (int q = 0; q < NR; ++q) {
-          float t = 0.f;
-#pragma unroll
-          for (int st = 0; st < S; ++st) t += x2_unit_dot(buf[p][q][st], lc, xa.w[st], xa.xs[st]);
-          v[q] = wave_sum_dpp(t);
-        }
-        if (i + PF < nrow) load_row(buf[p], i + PF);
-        if (lane == 0) {
-          int mat = 0, lrow = w + i * W;
-          if constexpr (MODE == kPlain) row_of(job, lrow, mat, lrow);
-          if constexpr (MODE == kResid) {
-            const float out = job.resid[lrow] + v[0];
-            job.resid[lrow] = out;
-            if (job.resid_bf16) job.resid_bf16[lrow] = f32_to_bf16_rne(out);
-          } else {
-            float out = v[0];
-            if constexpr (MODE == kSwiGLU) out = silu(v[0]) * v[1];
-            if (MODE == kPlain && job.bias) out += job.bias[lrow];
-            if (job.y[mat]) job.y[mat][lrow] = out;
-            if (job.yb[mat]) job.yb[mat][lrow] = f32_to_bf16_rne(out);
-          }
-        }
-      }
-    }
-  }
-}
-
-template <int MODE, int S, int PF>
-static int launch_x2p(const StreamJob& job, int blocks_per_cu, hipStream_t s) {
-  const size_t lds = tile_x_lds_bytes_q4k(job.k);
-  const int need = (job.rows + 3) / 4;
-  const int blocks = std::max(1, std::min(need, device_cus() * blocks_per_cu));
-  hipLaunchKernelGGL((gemv_x2p_kernel<MODE, S, PF>), dim3(blocks), dim3(256), lds, s, job);
-  return check_launch("gemv_x2p");
 }
 
 template <int QT, bool DL, int MODE, int R, int OCC = 1, bool ALLOW_FULL = true, bool XL = false>

@@ -34,22 +34,26 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-template <int CTRL>
+template <int CTRL, int ROWS = 0xF>
 __device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false));
 }
 
-// Sum over the 64 lanes, result in every lane: DPP within rows of 16 lanes
-// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror),
-// then two cross-row exchanges.
+// Sum over the 64 lanes, the same value in every lane: DPP within rows of 16
+// lanes (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror: every lane then holds its row's sum s_r), then row_bcast:15 into
+// rows 1 and 3 (s1 + s0, s3 + s2) and row_bcast:31 into rows 2 and 3, so lane
+// 63 holds (s3 + s2) + (s1 + s0), read out as a wave-uniform value.  No LDS
+// round trip; the bits equal a butterfly over lanes 16 and 32 (float addition
+// is commutative, so every lane of the butterfly holds this same sum).
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += dpp_f<0xB1>(v);
   v += dpp_f<0x4E>(v);
   v += dpp_f<0x141>(v);
   v += dpp_f<0x140>(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  v += dpp_f<0x142, 0xA>(v);
+  v += dpp_f<0x143, 0xC>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // Sum over a 256-thread workgroup (4 waves), result in every thread; red:

@@ -698,7 +698,10 @@ inline bool x1p_ok(int qtype, const StreamJob& job, bool xbf16) {
 // The fused-RMSNorm launch (job.x float32, job.norm_w set); x1p_ok must hold.
 template <int MODE>
 static int gemv_dispatch_norm(int qtype, bool d_last, const StreamJob& job, hipStream_t s) {
-  const int bpc = job.rows >= 8192 ? 4 : 3;
+  // two workgroups per CU (measured against 1-5 per CU on the q/k/v, gate/up
+  // and lm_head launches of the Llama-3-8B step: q/k/v 7.33 us vs 7.78 at
+  // three, gate/up 14.7 vs 15.6 at four, lm_head 77.4 vs 78.4 at four)
+  constexpr int bpc = 2;
   if (qtype == kQ4_K) return launch_x1p<kQ4_K, false, MODE, 1, true>(job, bpc, s);
   return d_last ? launch_x1p<kQ6_K, true, MODE, 1, true>(job, bpc, s)
                 : launch_x1p<kQ6_K, false, MODE, 1, true>(job, bpc, s);
@@ -710,10 +713,13 @@ static int gemv_dispatch_mode(int qtype, bool d_last, const StreamJob& job, bool
   for (int i = 0; i < job.n_mats; ++i)
     if ((int64_t)job.n[i] * job.row_bytes >= ((int64_t)1 << 31)) x1 = false;  // 32-bit buffer offsets
   if (x1 && job.k <= 4096) {
-    // one row in flight ahead of the math; four workgroups per CU for long
-    // matrices, three below 8192 rows (measured: 14336 x 4096 Q4_K 8.6 us at
-    // four, 4096 x 4096 5.5 us at three vs 5.8 at four)
-    const int bpc = job.rows >= 8192 ? 4 : 3;
+    // one row in flight ahead of the math.  Single-matrix launches: four
+    // workgroups per CU for long matrices, three below 8192 rows (measured:
+    // 14336 x 4096 Q4_K 8.6 us at four vs 9.0 at two, 12288 rows 7.9 at four
+    // vs 8.1 at three).  Launches that move two rows per item (kSwiGLU) or end
+    // in the residual update: two per CU (gate/up 2 x 14336 x 4096 14.7 us vs
+    // 15.6 at four, o 4096 x 4096 5.0 vs 5.1 at three)
+    const int bpc = (MODE == kSwiGLU || MODE == kResid) ? 2 : job.rows >= 8192 ? 4 : 3;
     if (qtype == kQ4_K) return launch_x1p<kQ4_K, false, MODE, 1>(job, bpc, s);
     return d_last ? launch_x1p<kQ6_K, true, MODE, 1>(job, bpc, s) : launch_x1p<kQ6_K, false, MODE, 1>(job, bpc, s);
   }
@@ -725,7 +731,7 @@ static int gemv_dispatch_mode(int qtype, bool d_last, const StreamJob& job, bool
     // multi-step form
     const int steps = ((job.k >> 6) + 63) >> 6;
     if (x1 && steps >= 2 && steps <= 4 && job.k % 256 == 0 && x1p_lds_bytes(qtype, job.k) <= 64 * 1024) {
-      constexpr int bpc = 3;
+      constexpr int bpc = 2;  // Q6_K 4096 x 14336: 14.6 us at two per CU, 14.7 at three, 15.3 at four
 #define DRACO_X1S(S_)                                                                      \
   if (steps == S_) {                                                                       \
     if (qtype == kQ4_K) return launch_x1s<kQ4_K, false, MODE, S_>(job, bpc, s);             \

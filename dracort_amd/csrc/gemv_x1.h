@@ -251,6 +251,12 @@ __device__ __forceinline__ void x1_fetch_x_rmsnorm(const float* __restrict__ h, 
   }
 }
 
+// The slots are computed for every chunk (clamped) and chosen by a select:
+// a slot computed only for chunks inside the row put each store behind a
+// branch, and the compiler then sank each chunk's load next to its store and
+// waited on it there -- eight serialized loads in the 14336-wide down
+// projection (Q6_K 4096 x 14336: 14.8 us, 14.1 with the loads issued together;
+// Q4_K 10.8 -> 10.5 us).
 template <int QT, int XC>
 __device__ __forceinline__ void x1_stage_regs(uint4* lds, const uint4 (&xr)[XC], int k) {
   const int chunks = k >> 3;
@@ -258,7 +264,9 @@ __device__ __forceinline__ void x1_stage_regs(uint4* lds, const uint4 (&xr)[XC],
 #pragma unroll
   for (int j = 0; j < XC; ++j) {
     const int c = (int)threadIdx.x + 256 * j;
-    lds[c < chunks ? (c >> 9) * 512 + x1_slot_of_chunk<QT>(c & 511) : pad + (int)threadIdx.x] = xr[j];
+    const int cc = min(c, chunks - 1);
+    const int slot = (cc >> 9) * 512 + x1_slot_of_chunk<QT>(cc & 511);
+    lds[c < chunks ? slot : pad + (int)threadIdx.x] = xr[j];
   }
   __syncthreads();
   x1_stage_sums<QT>(lds, k);

@@ -56,6 +56,9 @@ struct StreamJob {
   const float* norm_w;
   float norm_eps;
   uint16_t* x_norm;
+  // bytes between activation rows (0: k elements); set when the launch covers a
+  // K window of longer rows (streaming kernel with the activations in LDS only)
+  int64_t x_stride;
 };
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
@@ -113,7 +116,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(StreamJob job, int row
   const int k = job.k;
   const int units = k >> 5;
   const int iters = (units + 63) >> 6;  // steps per row
-  const size_t xstride = XBF16 ? (size_t)k * 2 : (size_t)k * 4;
+  const size_t xstride = job.x_stride ? (size_t)job.x_stride : XBF16 ? (size_t)k * 2 : (size_t)k * 4;
   const uint8_t* xb = static_cast<const uint8_t*>(job.x);
 
   // LDS: [x rows (XLDS)][group sums (XLDS)][per-wave row results]
@@ -440,6 +443,50 @@ static int stream_dispatch(int qtype, bool d_last, const StreamJob& job, bool xb
       if constexpr (MODE == kSwiGLU) return stream_ext_swiglu(qtype, d_last, job, xbf16, s);
       return stream_ext_resid(qtype, d_last, job, xbf16, s);
   }
+}
+
+// Activation rows too long for the LDS image (M * K * sizeof(x) > 64 KB, e.g.
+// float32 rows of 4 x 14336 or 8 x 4096): without it the streaming kernel
+// reads each lane's activations from global memory again for every row.
+// Instead the launch is split into K windows of whole 2048-element steps, each
+// small enough for the image: window w multiplies columns [k_w, k_w + K_w) of
+// every row (the weight base moves by those columns' blocks, the row stride
+// stays) with the same columns of x (x_stride keeps the full row).  The first
+// window writes y (plain, with the bias) or adds into resid; every later one
+// adds into that output through the residual epilogue; the bf16 copy is
+// written by the last.  Single-matrix plain launches with a float32 output and
+// residual launches only.
+inline int stream_window_k(const StreamJob& job, bool xbf16) {
+  const int mt = job.m <= 1 ? 1 : job.m <= 2 ? 2 : job.m <= 4 ? 4 : job.m <= 8 ? 8 : 16;
+  const size_t xb = xbf16 ? 2 : 4;
+  if ((size_t)mt * job.k * xb <= kStreamMaxLds || job.k % 2048 != 0) return 0;
+  return (int)(kStreamMaxLds / ((size_t)mt * xb)) / 2048 * 2048;
+}
+
+template <int MODE>
+static int stream_windowed(int qtype, bool d_last, const StreamJob& job, bool xbf16, int kw, hipStream_t s) {
+  static_assert(MODE != kSwiGLU, "the SwiGLU epilogue is not additive");
+  const size_t xb = xbf16 ? 2 : 4;
+  for (int k0 = 0; k0 < job.k; k0 += kw) {
+    const bool first = k0 == 0, last = k0 + kw >= job.k;
+    StreamJob w = job;
+    w.k = std::min(kw, job.k - k0);
+    w.x = static_cast<const uint8_t*>(job.x) + (size_t)k0 * xb;
+    w.x_stride = (int64_t)job.k * (int64_t)xb;
+    w.w[0] = job.w[0] + row_bytes_of(qtype, k0);
+    int rc;
+    if (MODE == kPlain && first) {
+      w.yb[0] = last ? job.yb[0] : nullptr;
+      rc = stream_dispatch<kPlain>(qtype, d_last, w, xbf16, s);
+    } else {
+      w.bias = nullptr;
+      w.resid = MODE == kResid ? job.resid : job.y[0];
+      w.resid_bf16 = last ? (MODE == kResid ? job.resid_bf16 : job.yb[0]) : nullptr;
+      rc = stream_dispatch<kResid>(qtype, d_last, w, xbf16, s);
+    }
+    if (rc) return rc;
+  }
+  return DRACO_OK;
 }
 
 }  // namespace draco

@@ -731,6 +731,17 @@ static int gemv_dispatch_mode(int qtype, bool d_last, const StreamJob& job, bool
     if (qtype == kQ4_K) return launch_x1p<kQ4_K, false, MODE, 1>(job, bpc, s);
     return d_last ? launch_x1p<kQ6_K, true, MODE, 1>(job, bpc, s) : launch_x1p<kQ6_K, false, MODE, 1>(job, bpc, s);
   }
+  // activation rows too long for the LDS image: the streaming kernel over K
+  // windows -- bf16 rows below 8, float32 rows up to 4, and 5..8 float32
+  // rows when two windows cover K (Q4_0 14336 x 4096, 8 rows: 94 -> 51 us;
+  // 4096 x 14336, 4 rows: 106 -> 54 us; 8 rows over seven windows was slower
+  // than the matrix cores below, 101 against 84 us)
+  if constexpr (MODE != kSwiGLU) {
+    const int kw = stream_window_k(job, xbf16);
+    const bool rows_ok = xbf16 ? job.m < 8 : (job.m <= 4 || (job.m <= 8 && job.k <= 2 * kw));
+    if (rows_ok && kw >= 2048 && (MODE == kResid || (job.n_mats == 1 && job.y[0])))
+      return stream_windowed<MODE>(qtype, d_last, job, xbf16, kw, s);
+  }
   // 8..16 activation rows: the matrix-core kernel (measured faster than the
   // streaming kernel from 8 rows on; at 4 rows they tie or the latter wins)
   if (job.m >= 8 && mfma_gemv_ok(qtype, job, xbf16)) return gemv_mfma_dispatch<MODE>(qtype, d_last, job, xbf16, s);

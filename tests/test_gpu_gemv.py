@@ -100,3 +100,42 @@ def test_gemv_single_token_multi_step_rows(qtype):
     r = resid.cuda()
     gguf_gemv_residual(x.cuda(), torch.from_numpy(blocks).cuda(), qtype, (640, 11008), r)
     check_close(r.cpu().numpy(), ref, f"{qtype:#x} residual")
+
+
+def _bf16_round(a: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16).float().numpy()
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0, Q4_K, Q6_K])
+@pytest.mark.parametrize("m", [2, 4, 8])
+def test_gemv_k_windows(qtype, m):
+    """Float32 activation rows longer than the LDS activation image (m x k
+    floats > 64 KB): the launch runs as K windows of whole 2048-column steps --
+    bias added by the first window, later windows through the residual
+    epilogue, the bf16 copy written by the last.  Eight rows are windowed only
+    when two windows cover K."""
+    from dracort_amd.kernels import gguf_gemv_multi, gguf_gemv_residual
+
+    n, k = 1000, (14336 if m <= 4 else 4096)
+    print(f"k windows {NAMES[qtype]} m={m}", flush=True)
+    y, ref = _run(qtype, n, k, m, torch.float32, seed=80 + m, bias=True)
+    check_close(y, ref, f"windows bias {NAMES[qtype]} m={m}")
+
+    blocks, w = quantized(qtype, n, k, 90 + m)
+    q = torch.from_numpy(blocks).cuda()
+    x = activations(m, k, 90 + m, torch.float32)
+    ref = matmul_ref.linear_ref(x.numpy(), w)
+    yo = torch.full((m, n), float("nan"), device="cuda")
+    yb = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+    gguf_gemv_multi(x.cuda(), [(q, n)], qtype, k, [yo], [yb])
+    got = yo.cpu().numpy()
+    check_close(got, ref, f"windows multi {NAMES[qtype]} m={m}")
+    assert np.array_equal(yb.float().cpu().numpy(), _bf16_round(got))
+
+    r0 = np.random.default_rng(95 + m).standard_normal((m, n), dtype=np.float32)
+    resid = torch.from_numpy(r0.copy()).cuda()
+    rb = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+    gguf_gemv_residual(x.cuda(), q, qtype, (n, k), resid, rb)
+    got = resid.cpu().numpy()
+    check_close(got, r0.astype(np.float64) + ref, f"windows residual {NAMES[qtype]} m={m}")
+    assert np.array_equal(rb.float().cpu().numpy(), _bf16_round(got))

@@ -335,9 +335,14 @@ __global__ __launch_bounds__(512) void moe_up_mfp_kernel(ExpertPtrs wg, ExpertPt
 // yk[off + t0 + m, :] = h[off + t0 + m, :] W_down[e]^T, 16 assignment rows per
 // pass; h arrives as the three bf16 planes the up kernels wrote (three MFMAs
 // per group against exact codes, no split here).
-template <int QT>
+//
+// NR 16-row weight tiles per workgroup share each wave's activation fragments
+// (the h planes, re-read from L2 / the Infinity Cache by every row tile of
+// the expert: 16 tokens x 14336 x 3 planes x 2 B = 1.4 MB per tile against
+// 129 KB of Q4_K weights), so NR = 2 halves that traffic.
+template <int QT, int NR>
 __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertPtrs wd, int H, int I, MoeWs ws) {
-  __shared__ mf_f32x4 part[4][64];
+  __shared__ mf_f32x4 part[4][NR][64];
   const int e = blockIdx.y;
   const int cnt = ws.counts[e];
   if (cnt == 0) return;
@@ -345,29 +350,37 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertPtrs wd, int H
   const int lane = threadIdx.x & 63;
   const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int q = lane >> 4, nl = lane & 15;
-  const int row0 = blockIdx.x * 16;  // H is a multiple of 16 and the grid covers it exactly
+  const int row0 = blockIdx.x * 16 * NR;  // H is a multiple of 16 NR and the grid covers it exactly
   const uint32_t row_bytes = (uint32_t)(I / Fmt<QT>::QK) * Fmt<QT>::BYTES;
-  const __amdgpu_buffer_rsrc_t rs[1] = {make_rsrc(wd.p[e], (uint32_t)H * row_bytes)};
-  const int rowoff = (int)((uint32_t)(row0 + nl) * row_bytes);
+  __amdgpu_buffer_rsrc_t rs[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) rs[r] = make_rsrc(wd.p[e] + (size_t)(row0 + 16 * r) * row_bytes, 16u * row_bytes);
+  const int rowoff = (int)((uint32_t)nl * row_bytes);
   for (int t0 = 16 * (int)blockIdx.z; t0 < cnt; t0 += 16 * (int)gridDim.z) {
     const int mt = min(16, cnt - t0);
     const uint16_t* xrow = ws.hp + (size_t)(off + t0 + min(nl, mt - 1)) * I;
-    mf_f32x4 acc[1] = {{0.f, 0.f, 0.f, 0.f}};
-    mf_accumulate<QT, false, 1, true>(rs, rowoff, xrow, q, ks, I >> 8, acc, ws.hp_plane);
-    part[ks][lane] = acc[0];
+    mf_f32x4 acc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+    mf_accumulate<QT, false, NR, true>(rs, rowoff, xrow, q, ks, I >> 8, acc, ws.hp_plane);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) part[ks][r][lane] = acc[r];
     __syncthreads();
     if (ks == 0) {
-      mf_f32x4 tot = part[0][lane];
 #pragma unroll
-      for (int j = 1; j < 4; ++j) {
-        const mf_f32x4 p = part[j][lane];
+      for (int r = 0; r < NR; ++r) {
+        mf_f32x4 tot = part[0][r][lane];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) tot[v] += p[v];
-      }
+        for (int j = 1; j < 4; ++j) {
+          const mf_f32x4 p = part[j][r][lane];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = 4 * q + v;
-        if (m < mt) ws.yk[(size_t)(off + t0 + m) * H + row0 + nl] = tot[v];
+          for (int v = 0; v < 4; ++v) tot[v] += p[v];
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = 4 * q + v;
+          if (m < mt) ws.yk[(size_t)(off + t0 + m) * H + row0 + 16 * r + nl] = tot[v];
+        }
       }
     }
     __syncthreads();
@@ -416,8 +429,8 @@ static int launch_moe(const ExpertPtrs& wg, const ExpertPtrs& wu, const ExpertPt
         hipLaunchKernelGGL((moe_up_mfma_kernel<QT, false>), dim3((unsigned)(I / 16), (unsigned)E, zt), dim3(256), 0, s,
                            wg, wu, x, H, I, ws);
       if (int rc = check_launch("moe_up_mfma")) return rc;
-      hipLaunchKernelGGL((moe_down_mfma_kernel<QT>), dim3((unsigned)(H / 16), (unsigned)E, zt), dim3(256), 0, s, wd, H,
-                         I, ws);
+      hipLaunchKernelGGL((moe_down_mfma_kernel<QT, 4>), dim3((unsigned)(H / 64), (unsigned)E, zt), dim3(256), 0, s, wd,
+                         H, I, ws);
       if (int rc = check_launch("moe_down_mfma")) return rc;
       hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, s, y,
                          H, k, ws);

@@ -232,15 +232,15 @@ __device__ __forceinline__ void mf_split3(float v, uint16_t& hi, uint16_t& mid, 
 }
 
 // acc (the lane's 4 values of the 16 x 16 tile) += the products over the
-// 256-element chunks ks, ks + 4, ... < chunks of NR weight rows (buffer
+// 256-element chunks ks, ks + KS, ... < chunks of NR weight rows (buffer
 // resources rs, the lane's row at byte offset rowoff) with the lane's
-// activation row xrow.  Software pipeline: the activations and codes of chunk
-// c + 4 are loaded while chunk c is multiplied.
+// activation row xrow (KS waves split K).  Software pipeline: the activations
+// and codes of chunk c + KS are loaded while chunk c is multiplied.
 //
 // XPL: the activations are already three bf16 planes (hi, mid, lo of a float32
 // row, as mf_split3 writes them) at xrow, xrow + pstride, xrow + 2 pstride
 // (uint16 elements); no split on the fly.
-template <int QT, bool XBF16, int NR, bool XPL = false>
+template <int QT, bool XBF16, int NR, bool XPL = false, int KS = 4>
 __device__ __forceinline__ void mf_accumulate(const __amdgpu_buffer_rsrc_t (&rs)[NR], int rowoff,
                                               const void* __restrict__ xrow, int q, int ks, int chunks,
                                               mf_f32x4 (&acc)[NR], size_t pstride = 0) {
@@ -267,11 +267,11 @@ __device__ __forceinline__ void mf_accumulate(const __amdgpu_buffer_rsrc_t (&rs)
   };
   auto compute_chunk = [&](int slot) { mf_chunk_q4<QT, XBF16, NR>(xb[slot], wb[slot], q, acc); };
   if (ks < chunks) load_chunk(0, ks);
-  for (int c = ks; c < chunks; c += 8) {
-    if (c + 4 < chunks) load_chunk(1, c + 4);
+  for (int c = ks; c < chunks; c += 2 * KS) {
+    if (c + KS < chunks) load_chunk(1, c + KS);
     compute_chunk(0);
-    if (c + 4 >= chunks) break;
-    if (c + 8 < chunks) load_chunk(0, c + 8);
+    if (c + KS >= chunks) break;
+    if (c + 2 * KS < chunks) load_chunk(0, c + 2 * KS);
     compute_chunk(1);
   }
 
@@ -355,7 +355,7 @@ __device__ __forceinline__ void mf_chunk_q6(const uint2 (&x)[16], const MfQ6 (&w
   }
 }
 
-template <bool DL, int NR>
+template <bool DL, int NR, int KS = 4>
 __device__ __forceinline__ void mf_accumulate_q6k(const __amdgpu_buffer_rsrc_t (&rs)[NR], int rowoff,
                                                   const void* __restrict__ xrow, int q, int ks, int chunks,
                                                   mf_f32x4 (&acc)[NR]) {
@@ -370,24 +370,26 @@ __device__ __forceinline__ void mf_accumulate_q6k(const __amdgpu_buffer_rsrc_t (
   };
   auto compute_chunk = [&](int slot) { mf_chunk_q6<NR>(xb[slot], wb[slot], acc); };
   if (ks < chunks) load_chunk(0, ks);
-  for (int c = ks; c < chunks; c += 8) {
-    if (c + 4 < chunks) load_chunk(1, c + 4);
+  for (int c = ks; c < chunks; c += 2 * KS) {
+    if (c + KS < chunks) load_chunk(1, c + KS);
     compute_chunk(0);
-    if (c + 4 >= chunks) break;
-    if (c + 8 < chunks) load_chunk(0, c + 8);
+    if (c + KS >= chunks) break;
+    if (c + 2 * KS < chunks) load_chunk(0, c + 2 * KS);
     compute_chunk(1);
   }
 }
 
-template <int QT, bool DL, bool XBF16, int MODE, int TPW>
-__global__ __launch_bounds__(TPW * 256) void gemv_mfma_kernel(StreamJob job) {
+// KS waves split K per tile (4, or 8 where there are too few tiles to give
+// every CU more than four waves: 4096 x 14336, 256 tiles).
+template <int QT, bool DL, bool XBF16, int MODE, int TPW, int KS = 4>
+__global__ __launch_bounds__(TPW * KS * 64) void gemv_mfma_kernel(StreamJob job) {
   constexpr int NR = MODE == kSwiGLU ? 2 : 1;
-  __shared__ mf_f32x4 part[TPW][4][NR][64];
+  __shared__ mf_f32x4 part[TPW][KS][NR][64];
   const int lane = threadIdx.x & 63;
   // wave-uniform indices in scalar registers (the buffer resources built from
   // them must be uniform, or every load becomes a waterfall loop)
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int t = wid >> 2, ks = wid & 3;
+  const int t = wid / KS, ks = wid % KS;
   const int row0 = (blockIdx.x * TPW + t) * 16;
   const int q = lane >> 4, nl = lane & 15;
   const int k = job.k, M = job.m;
@@ -412,11 +414,11 @@ __global__ __launch_bounds__(TPW * 256) void gemv_mfma_kernel(StreamJob job) {
   for (int r = 0; r < NR; ++r) acc[r] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
   const void* xrow = static_cast<const uint8_t*>(job.x) + (size_t)min(nl, M - 1) * k * (XBF16 ? 2 : 4);
   if constexpr (QT == kQ6_K)
-    mf_accumulate_q6k<DL, NR>(rs, rowoff, xrow, q, ks, chunks, acc);
+    mf_accumulate_q6k<DL, NR, KS>(rs, rowoff, xrow, q, ks, chunks, acc);
   else
-    mf_accumulate<QT, XBF16, NR>(rs, rowoff, xrow, q, ks, chunks, acc);
+    mf_accumulate<QT, XBF16, NR, false, KS>(rs, rowoff, xrow, q, ks, chunks, acc);
 
-  // sum the four K-split partial tiles
+  // sum the KS partial tiles
 #pragma unroll
   for (int r = 0; r < NR; ++r) part[t][ks][r][lane] = acc[r];
   __syncthreads();
@@ -426,7 +428,7 @@ __global__ __launch_bounds__(TPW * 256) void gemv_mfma_kernel(StreamJob job) {
   for (int r = 0; r < NR; ++r) {
     tot[r] = part[t][0][r][lane];
 #pragma unroll
-    for (int j = 1; j < 4; ++j) {
+    for (int j = 1; j < KS; ++j) {
       const mf_f32x4 p = part[t][j][r][lane];
 #pragma unroll
       for (int v = 0; v < 4; ++v) tot[r][v] += p[v];
@@ -692,7 +694,13 @@ static int launch_gemv_mfma(const StreamJob& job, hipStream_t s) {
       return check_launch("gemv_mfma");
     }
   }
-  hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 1>), dim3(tiles), dim3(256), 0, s, job);
+  // bf16: eight waves split K (two per SIMD; 4096 x 14336 Q6_K at 16 rows 44.9
+  // -> 42.4 us, at 8 rows 37.6 -> 34.6; Q4_K 25.8 -> 24.8); float32 activations
+  // need all 512 registers of a lane (one wave per SIMD), so four
+  if constexpr (XBF16)
+    hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 1, 8>), dim3(tiles), dim3(512), 0, s, job);
+  else
+    hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 1>), dim3(tiles), dim3(256), 0, s, job);
   return check_launch("gemv_mfma");
 }
 

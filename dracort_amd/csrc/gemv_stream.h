@@ -377,6 +377,9 @@ static int launch_stream_x(const StreamJob& job, hipStream_t s) {
     if (full) return launch_stream<QT, DL, MT, XBF16, MODE, true, true>(job, s);
     return launch_stream<QT, DL, MT, XBF16, MODE, true, false>(job, s);
   }
+  // the global-memory activation path indexes rows by k: a K window (x_stride
+  // set) must fit the LDS image
+  if (job.x_stride) return set_error(DRACO_EINVAL_SHAPE, "K window of %d columns does not fit the activation image", job.k);
   if (full) return launch_stream<QT, DL, MT, XBF16, MODE, false, true>(job, s);
   return launch_stream<QT, DL, MT, XBF16, MODE, false, false>(job, s);
 }
@@ -456,8 +459,15 @@ static int stream_dispatch(int qtype, bool d_last, const StreamJob& job, bool xb
 // adds into that output through the residual epilogue; the bf16 copy is
 // written by the last.  Single-matrix plain launches with a float32 output and
 // residual launches only.
-inline int stream_window_k(const StreamJob& job, bool xbf16) {
-  const int mt = job.m <= 1 ? 1 : job.m <= 2 ? 2 : job.m <= 4 ? 4 : job.m <= 8 ? 8 : 16;
+// The row tile MT the launch of this type will use (stream_mt / stream_mt_ext).
+inline int stream_tile_rows(int qtype, int m) {
+  const bool ext = !(qtype == kQ8_0 || qtype == kQ4_0 || qtype == kQ4_K || qtype == kQ6_K);
+  if (ext) return m <= 1 ? 1 : m <= 4 ? 4 : 16;
+  return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
+}
+
+inline int stream_window_k(int qtype, const StreamJob& job, bool xbf16) {
+  const int mt = stream_tile_rows(qtype, job.m);
   const size_t xb = xbf16 ? 2 : 4;
   if ((size_t)mt * job.k * xb <= kStreamMaxLds || job.k % 2048 != 0) return 0;
   return (int)(kStreamMaxLds / ((size_t)mt * xb)) / 2048 * 2048;

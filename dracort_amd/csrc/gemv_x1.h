@@ -737,9 +737,13 @@ static int gemv_dispatch_mode(int qtype, bool d_last, const StreamJob& job, bool
   // 4096 x 14336, 4 rows: 106 -> 54 us; 8 rows over seven windows was slower
   // than the matrix cores below, 101 against 84 us)
   if constexpr (MODE != kSwiGLU) {
-    const int kw = stream_window_k(job, xbf16);
+    const int kw = stream_window_k(qtype, job, xbf16);
     const bool rows_ok = xbf16 ? job.m < 8 : (job.m <= 4 || (job.m <= 8 && job.k <= 2 * kw));
-    if (rows_ok && kw >= 2048 && (MODE == kResid || (job.n_mats == 1 && job.y[0])))
+    // not the four-group formats: Q2_K / Q3_K / Q6_K at 4 bf16 rows of 14336
+    // were slower windowed (32.1 -> 46.8, 54.6 -> 56.1, 44.9 -> 50.1 us; the
+    // other seven types 1-14 % faster)
+    const bool type_ok = qtype != kQ2_K && qtype != kQ3_K && qtype != kQ6_K;
+    if (rows_ok && type_ok && kw >= 2048 && (MODE == kResid || (job.n_mats == 1 && job.y[0])))
       return stream_windowed<MODE>(qtype, d_last, job, xbf16, kw, s);
   }
   // 8..16 activation rows: the matrix-core kernel (measured faster than the

@@ -7,7 +7,7 @@ import torch
 
 from dracort_amd.kernels import gguf_gemv, gguf_linear
 from oracle import matmul_ref
-from tests.gguf_cases import NAMES, Q4_0, Q4_K, Q6_K, Q8_0, TYPES, activations, check_close, quantized
+from tests.gguf_cases import NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, TYPES, activations, check_close, quantized
 
 pytestmark = pytest.mark.gpu
 
@@ -106,14 +106,15 @@ def _bf16_round(a: np.ndarray) -> np.ndarray:
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16).float().numpy()
 
 
-@pytest.mark.parametrize("qtype", [Q4_0, Q8_0, Q4_K, Q6_K])
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0, Q4_K, Q5_K, Q6_K])
 @pytest.mark.parametrize("m", [2, 4, 8])
 def test_gemv_k_windows(qtype, m):
     """Float32 activation rows longer than the LDS activation image (m x k
     floats > 64 KB): the launch runs as K windows of whole 2048-column steps --
     bias added by the first window, later windows through the residual
     epilogue, the bf16 copy written by the last.  Eight rows are windowed only
-    when two windows cover K."""
+    when two windows cover K; Q6_K (like Q2_K / Q3_K) is not windowed and
+    checks the same entry points on its unwindowed path."""
     from dracort_amd.kernels import gguf_gemv_multi, gguf_gemv_residual
 
     n, k = 1000, (14336 if m <= 4 else 4096)

@@ -16,6 +16,8 @@ Printed (one JSON line on stdout):
              HIP events on its launch stream over a rotation of the 64 distinct
              gate/up matrices (2.1 GB, beyond the 256 MB Infinity Cache),
              algorithmic bytes per launch / average launch time, vs 8 TB/s
+  roofline_step_dominant  the same measurement for the launch that dominates
+             the step: the fused gate + up + SiLU.up GEMV (2 x 14336 x 4096)
   cpu_baseline  the reference CPU path (numpy dequant + float32 x @ W.T,
              as the oracle restates it) on the host cores, warm fp32-weight
              cache, one layer + 1/8 of lm_head timed and scaled to a step
@@ -103,6 +105,36 @@ def dominant_kernel_roofline(ls, reps):
         "avg_launch_us": round(ms * 1e3, 3),
         "launches_timed": reps * len(fns),
         "rotation": f"{len(mats)} distinct weights, {len(mats) * mats[0].nbytes / 1e9:.2f} GB (> 256 MB Infinity Cache)",
+    }
+
+
+def step_dominant_roofline(ls, reps):
+    """The launch that dominates the timed step: gate + up + SiLU.up of one
+    layer (2 x 14336 x 4096 Q4_K, M = 1, bf16 x) in one fused launch, timed
+    like the roofline kernel over the 32 layers' distinct gate/up pairs
+    (2.1 GB).  Reported beside ``roofline`` (the single 14336 x 4096 GEMV)."""
+    import torch
+
+    from dracort_amd.kernels import gguf_gemv_swiglu
+
+    pairs = [(layer["gate"], layer["up"]) for layer in ls.layers]
+    n, k = pairs[0][0].shape
+    x = torch.randn((1, k), device="cuda").to(torch.bfloat16)
+    y = torch.empty((1, n), device="cuda", dtype=torch.float32)
+    fns = [lambda g=g, u=u: gguf_gemv_swiglu(x, g.data, u.data, g.ggml_type, g.shape, out=y) for g, u in pairs]
+    ms = time_launches(fns, reps)
+    alg_bytes = 2 * pairs[0][0].nbytes + k * 2 + n * 4
+    achieved = alg_bytes / (ms * 1e-3) / 1e9
+    return {
+        "kernel": "gemv_x1p_kernel<Q4_K, kSwiGLU> (fused gate + up + SiLU.up, M = 1, bf16 x), 2 x 14336 x 4096 Q4_K",
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "alg_bytes_per_launch": alg_bytes,
+        "avg_launch_us": round(ms * 1e3, 3),
+        "launches_timed": reps * len(fns),
     }
 
 
@@ -472,6 +504,8 @@ def main() -> int:
 
     roof = dominant_kernel_roofline(ls, args.roofline_reps)
     log(f"roofline: {roof}")
+    dom = step_dominant_roofline(ls, args.roofline_reps)
+    log(f"step-dominant launch: {dom}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -509,6 +543,7 @@ def main() -> int:
         "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "full_decode": full,
         "roofline": roof,
+        "roofline_step_dominant": dom,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

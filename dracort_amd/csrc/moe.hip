@@ -339,7 +339,9 @@ __global__ __launch_bounds__(512) void moe_up_mfp_kernel(ExpertPtrs wg, ExpertPt
 // NR 16-row weight tiles per workgroup share each wave's activation fragments
 // (the h planes, re-read from L2 / the Infinity Cache by every row tile of
 // the expert: 16 tokens x 14336 x 3 planes x 2 B = 1.4 MB per tile against
-// 129 KB of Q4_K weights), so NR = 2 halves that traffic.
+// 129 KB of Q4_K weights), which cuts that traffic NR-fold; launched with
+// NR = 4 (Mixtral shape: 503, 287, 238 us for NR = 1, 2, 4; the extra
+// accumulators spill to AGPRs, not to scratch).
 template <int QT, int NR>
 __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertPtrs wd, int H, int I, MoeWs ws) {
   __shared__ mf_f32x4 part[4][NR][64];

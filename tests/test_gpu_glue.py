@@ -90,6 +90,15 @@ def test_decode_attention_long_cache_multi_step_waves():
     _attention_case(2, 8, 2, 64, 40000, [39999, 12345], 500000.0, True, seed=40)
 
 
+def test_decode_attention_batch16():
+    """16 sequences (the batch-16 decode step's attention launch: 16 x 8 kv
+    heads x 35 one-wave splits), positions at and around the 32-position split
+    edges, one per sequence."""
+    positions = [0, 31, 32, 63, 64, 95, 100, 255, 256, 511, 700, 1023, 1050, 1087, 1099, 5]
+    print("decode attention batch 16 max_pos 1100", flush=True)
+    _attention_case(16, 32, 8, 128, 1100, positions, 500000.0, True, seed=16)
+
+
 def test_decode_attention_bf16_out_and_invalid_position():
     print("decode attention bf16 out", flush=True)
     _attention_case(2, 32, 8, 128, 512, [17, 300], 500000.0, True, seed=9, out_dtype=torch.bfloat16)

@@ -184,6 +184,11 @@ def cpu_baseline(ls, step_bytes):
 
         t_layer = timed(layer_fn, 6.0)
         t_lm = timed(lambda: matmul_ref.cpu_linear_f32(x, wlm), 3.0)
+    # the same layer on one thread (the reference's default is OpenBLAS's own
+    # thread count; one thread is its floor)
+    with threadpool_limits(limits=1):
+        t_layer_1 = timed(layer_fn, 3.0)
+    layer_bytes = sum(w.nbytes for w in ls.layers[0].values())
     # one step = 32 layers + the full lm_head (8 x the timed 1/8 of its rows)
     step_warm = ls.shape.n_layers * t_layer + 8 * t_lm
     step_cold = step_warm + ls.shape.n_layers * t_dq_layer + 8 * t_dq_lm
@@ -202,6 +207,7 @@ def cpu_baseline(ls, step_bytes):
         "tokens_per_s_cold": round(1.0 / step_cold, 4),
         "dequant_s_layer": round(t_dq_layer, 3),
         "dequant_s_lm_part": round(t_dq_lm, 3),
+        "one_thread_layer_GB_s": round(layer_bytes / t_layer_1 / 1e9, 2),
     }
 
 

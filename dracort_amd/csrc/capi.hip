@@ -343,9 +343,8 @@ int draco_gguf_linear(int ggml_type, const void* w, size_t w_bytes, const void* 
   g_last_error[0] = 0;
   if (m < 1 || m > kMaxDim) return set_error(DRACO_EINVAL_SHAPE, "invalid token count %lld", (long long)m);
   if (x_dtype != DRACO_DTYPE_F32) return set_error(DRACO_EINVAL_ARG, "unknown activation dtype %d", x_dtype);
-  // float32 activations, many rows: 16-row GEMV tiles.  Tile row offsets keep x 16-byte aligned
-  // (k is a multiple of 32); y needs n % 4 == 0.
-  if (n % 4 != 0) return set_error(DRACO_EINVAL_SHAPE, "float32 activations with m > 16 need n divisible by 4");
+  // float32 activations, many rows: 16-row GEMV tiles.  Tile row offsets keep x and y 16-byte
+  // aligned: m0 is a multiple of 16, so x + m0 k and y + m0 n move by multiples of 64 bytes.
   for (int64_t m0 = 0; m0 < m; m0 += 16) {
     const int64_t mt = m - m0 < 16 ? m - m0 : 16;
     const float* xt = static_cast<const float*>(x) + m0 * k;

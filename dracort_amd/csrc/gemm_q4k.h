@@ -15,11 +15,14 @@
 // So y += d D1 - dmin D2 per super-block, two FMAs per output where the
 // per-sub-block form needs sixteen.
 //
-// The activations reach the kernel as f16 (exact for bf16 inputs in f16's
-// range) plus the sub-block sums, both written by gemm_prep_kernel: one
-// workgroup per token row finds the row's largest |x| and, above 2^15,
-// scales the row by a power of two (undone on the output), so f16 never
-// overflows.
+// The activations reach the kernel as f16 plus the sub-block sums, both
+// written by gemm_prep_kernel: one workgroup per token row finds the row's
+// largest |x| and scales the row by the power of two 2^-t that puts it in
+// [2^14, 2^15) (undone on the output through 2^t).  Up or down, so f16 never
+// overflows and a row of small values never falls into f16's subnormals: every
+// element within 2^-31 of the row's largest is exact in f16 (a bf16 value has 8
+// significant bits, f16 keeps them down to 2^-17), and the ones below that
+// contribute less than 2^-31 of the row's largest term to any output.
 //
 // Tiling: a 256-thread workgroup owns BM (64) tokens x 128 weight rows; its
 // four waves each own (BM / 2) x 64 outputs as 16 x 16 MFMA tiles.  Per K
@@ -97,10 +100,12 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const uint16_t* __restri
   if (lane == 0) wmax[wave] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  // keep |x| 2^-t below 2^15 (f16 tops out at 65504); NaN / inf rows pass unscaled
+  // |x| 2^-t in [2^14, 2^15) for every finite nonzero row (f16 tops out at
+  // 65504, its normals start at 2^-14); zero and NaN / inf rows pass unscaled.
+  // The scaling is an exponent shift (v_ldexp) per element: 2^-t itself can
+  // exceed float32's range for rows of subnormal bf16 values
   int t = 0;
-  if (mx > 32768.f && mx <= 3.0e38f) t = ilogbf(mx) - 14;
-  const float s = ldexpf(1.f, -t);
+  if (mx > 0.f && __builtin_isfinite(mx)) t = ilogbf(mx) - 14;
 
   const size_t plane = (size_t)M * groups;
   for (int g = tid; g < groups; g += 256) {
@@ -112,7 +117,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const uint16_t* __restri
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float f0 = __uint_as_float(w[i] << 16) * s, f1 = __uint_as_float(w[i] & 0xFFFF0000u) * s;
+        const float f0 = ldexpf(__uint_as_float(w[i] << 16), -t), f1 = ldexpf(__uint_as_float(w[i] & 0xFFFF0000u), -t);
         sum += f0;
         sum += f1;
         h[4 * c + i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f0, f1));

@@ -5,7 +5,10 @@ the classes this path raises, so callers that catch the reference's errors
 catch these: ``DracoFormatError`` for an unsupported ggml type, a row length
 that is not a multiple of the block size or a truncated payload
 (``draco/format/gguf.py:284-296``), ``KernelError`` for a kernel that is
-unavailable or fails (``draco/exceptions.py:45``).
+unavailable or fails (``draco/exceptions.py:45``), ``KVCacheError`` for a
+decode step past the end of its KV cache (``draco/exceptions.py:61``),
+``CPUError`` for executor-level errors such as a missing weight tensor
+(``draco/exceptions.py:85``).
 """
 
 from __future__ import annotations
@@ -25,3 +28,11 @@ class KernelError(DracoError):
 
 class DracoFormatError(DracoError):
     """Raised when GGUF block data is malformed or of an unsupported type."""
+
+
+class KVCacheError(DracoError):
+    """Raised when the KV cache cannot take another token."""
+
+
+class CPUError(DracoError):
+    """Raised by the executor (name kept from the reference's CPU executor errors)."""

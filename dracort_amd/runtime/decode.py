@@ -31,6 +31,7 @@ from typing import Dict, List, Optional
 
 import torch
 
+from dracort_amd.exceptions import KVCacheError
 from dracort_amd.format.gguf import GGML_TYPE_Q4_K, GGML_TYPE_Q6_K, tensor_bytes
 from dracort_amd.kernels.glue import DecodeAttentionWorkspace, decode_attention, rms_norm, rope_tables
 from dracort_amd.kernels.gguf import (
@@ -133,7 +134,12 @@ def layer_set_bytes(shape: LlamaShape, types=None, lm_head_type: int = GGML_TYPE
 class DecodeStep:
     """Preallocated buffers + the decode chain for a batch of `m` tokens (one
     per sequence); ``attention`` selects the full step (see the module doc),
-    with ``start_position`` tokens already cached per sequence."""
+    with ``start_position`` tokens already cached per sequence.
+
+    The full step keeps a host-side count of the position it will write next
+    (the device positions advance by one per step, eager or replayed): a step
+    that would write position ``max_positions`` raises ``KVCacheError`` before
+    anything is enqueued."""
 
     def __init__(self, ls: LayerSet, m: int = 1, device="cuda", attention: Optional[AttentionShape] = None,
                  start_position: int = 0) -> None:
@@ -163,6 +169,7 @@ class DecodeStep:
             self.k_cache = [torch.zeros(cache, dtype=torch.float16, device=device) for _ in ls.layers]
             self.v_cache = [torch.zeros(cache, dtype=torch.float16, device=device) for _ in ls.layers]
             self.positions = torch.full((m,), start_position, dtype=torch.int32, device=device)
+            self.next_position = start_position
             self.rope = rope_tables(a.head_dim, a.max_positions, a.rope_theta, device)
             self.ws = DecodeAttentionWorkspace(m, a.n_heads, a.n_kv_heads, a.head_dim, a.max_positions, device)
             self.qf = torch.empty((m, s.hidden), **f32)
@@ -193,8 +200,15 @@ class DecodeStep:
         gguf_gemv(self.h_bf16, w.data, w.ggml_type, w.shape, out=self.logits)
         return self.logits
 
+    def _claim_position(self) -> None:
+        if self.next_position >= self.attn.max_positions:
+            raise KVCacheError(f"KV cache full: position {self.next_position} is past max_positions "
+                               f"{self.attn.max_positions}")
+        self.next_position += 1
+
     def _run_full(self) -> torch.Tensor:
         s, a = self.ls.shape, self.attn
+        self._claim_position()
         self.h.copy_(self.x_in)
         for li, layer in enumerate(self.ls.layers):
             norms = self.ls.norms[li]
@@ -222,18 +236,31 @@ class DecodeStep:
         return self.logits
 
     def capture(self) -> None:
-        """Capture one step into a HIP graph (replay with ``replay``)."""
+        """Capture one step into a HIP graph (replay with ``replay``).
+
+        One eager step runs first (allocator and library warm-up).  For the
+        full step its only lasting effect is undone: the device positions and
+        the host count are put back, so the first replay writes the same
+        position again (overwriting the warm-up's cache entry)."""
+        saved = self.positions.clone() if self.attn is not None else None
+        saved_next = self.next_position if self.attn is not None else None
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             self.run()  # warm the allocator / library outside capture
+            if saved is not None:
+                self.positions.copy_(saved)
         torch.cuda.current_stream().wait_stream(s)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             self.run()
+        if saved_next is not None:
+            self.next_position = saved_next  # capturing enqueues nothing
         self.graph = g
 
     def replay(self) -> torch.Tensor:
         assert self.graph is not None
+        if self.attn is not None:
+            self._claim_position()
         self.graph.replay()
         return self.logits

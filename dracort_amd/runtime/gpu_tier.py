@@ -11,8 +11,15 @@ weight_bytes)``) and are held in a ``KernelSelection``
 (``draco/runtime/cpu/dispatcher.py:30-35``).
 
 :class:`GGUFGpuKernel` is that kind of object for the MI355X path.  It keeps
-each GGUF weight's packed blocks resident in HBM after first use (keyed by
-tensor name and file offset) and runs ``gguf_linear`` on them:
+each GGUF weight's packed blocks resident in HBM after first use and runs
+``gguf_linear`` on them.  A tier object may serve several readers (the
+reference keeps its kernels as process-wide singletons,
+``draco/runtime/cpu/dispatcher.py:25``), so the residency cache is keyed on
+where the bytes come from, never on the tensor name alone: for ``linear`` the
+file (real path, device, inode, size, modification time), the tensor name, its
+offset and the kernel type (which carries the Q2_K / Q3_K / Q6_K field order);
+for ``matmul`` the tensor name, kernel type, shape and a 128-bit hash of the
+``weight_bytes`` handed in, so changed bytes are always uploaded again.
 
 * ``matmul(activation, tensor_info, weight_bytes)`` -- the reference
   signature: numpy activations in, numpy float32 out (host <-> device copies
@@ -30,7 +37,9 @@ GPU every call raises.
 
 from __future__ import annotations
 
-from typing import Callable, Dict, Optional, Tuple, Union
+import hashlib
+import os
+from typing import Callable, Dict, Hashable, Optional, Tuple, Union
 
 import numpy as np
 import torch
@@ -42,6 +51,38 @@ from dracort_amd.kernels.gguf import gguf_linear
 from dracort_amd.quantization.gguf import GGUFQuantizedWeight
 
 Array = Union[np.ndarray, torch.Tensor]
+
+try:  # a fast 128-bit hash of the weight bytes (matmul's cache key); hashlib otherwise
+    import xxhash
+
+    def _digest(buf) -> bytes:
+        return xxhash.xxh3_128_digest(buf)
+except ImportError:  # pragma: no cover - xxhash ships with this image
+    def _digest(buf) -> bytes:
+        return hashlib.blake2b(buf, digest_size=16).digest()
+
+
+def reader_key(reader) -> Hashable:
+    """Identity of the file behind a reader: (real path, st_dev, st_ino, size,
+    mtime_ns); a reader without a path is identified by the object itself."""
+    path = getattr(reader, "path", None)
+    if isinstance(path, (str, bytes, os.PathLike)):
+        try:
+            st = os.stat(path)
+            return ("file", os.path.realpath(path), st.st_dev, st.st_ino, st.st_size, st.st_mtime_ns)
+        except OSError:
+            pass
+    return ("reader", id(reader))
+
+
+def linear_weight_key(reader, info, kernel_type: int) -> Hashable:
+    return (reader_key(reader), info.name, int(info.offset), int(kernel_type))
+
+
+def bytes_weight_key(info, kernel_type: int, weight_bytes) -> Hashable:
+    buf = weight_bytes if isinstance(weight_bytes, (bytes, bytearray, memoryview)) else \
+        np.ascontiguousarray(weight_bytes).view(np.uint8)
+    return ("bytes", info.name, int(kernel_type), tuple(info.shape), _digest(buf))
 
 
 def is_gguf_block_tensor(info) -> bool:
@@ -57,7 +98,7 @@ class GGUFGpuKernel:
 
     def __init__(self, device: Union[str, torch.device] = "cuda") -> None:
         self.device = torch.device(device)
-        self._weights: Dict[Tuple[str, int], GGUFQuantizedWeight] = {}
+        self._weights: Dict[Hashable, Union[GGUFQuantizedWeight, torch.Tensor]] = {}
 
     @property
     def name(self) -> str:
@@ -71,12 +112,13 @@ class GGUFGpuKernel:
         return is_gguf_block_tensor(info)
 
     # -- weights ---------------------------------------------------------
-    def resident_weight(self, info, kernel_type: int, fetch: Callable[[], object]) -> GGUFQuantizedWeight:
-        """The HBM copy of a tensor's packed blocks; ``fetch()`` gives the
-        payload (bytes or a uint8 array) and is called on first use only."""
+    def resident_weight(self, key: Hashable, info, kernel_type: int,
+                        fetch: Callable[[], object]) -> GGUFQuantizedWeight:
+        """The HBM copy of a tensor's packed blocks under cache key ``key``;
+        ``fetch()`` gives the payload (bytes or a uint8 array) and is called
+        on first use of the key only."""
         if not is_gguf_block_tensor(info):
             raise KernelError(f"tensor '{getattr(info, 'name', '?')}' is not a GGUF block tensor this tier runs")
-        key = (info.name, int(info.offset))
         w = self._weights.get(key)
         if w is None:
             if not torch.cuda.is_available():
@@ -97,14 +139,15 @@ class GGUFGpuKernel:
     # -- reference kernel interface --------------------------------------
     def matmul(self, activation: np.ndarray, tensor_info, weight_bytes) -> np.ndarray:
         """``activation @ W.T`` for ``activation`` [M, K] (numpy) -> float32 [M, N] (numpy)."""
-        w = self.resident_weight(tensor_info, tensor_info.ggml_type, lambda: weight_bytes)
+        key = bytes_weight_key(tensor_info, tensor_info.ggml_type, weight_bytes)
+        w = self.resident_weight(key, tensor_info, tensor_info.ggml_type, lambda: weight_bytes)
         x = torch.from_numpy(np.ascontiguousarray(activation, dtype=np.float32)).to(self.device)
         return gguf_linear(x, w.data, w.ggml_type, w.shape).cpu().numpy()
 
     # -- _linear ---------------------------------------------------------
     def linear(self, reader, name: str, x: Array, bias_name: Optional[str] = None) -> Array:
         info, kernel_type, fetch = _describe(reader, name)
-        w = self.resident_weight(info, kernel_type, fetch)
+        w = self.resident_weight(linear_weight_key(reader, info, kernel_type), info, kernel_type, fetch)
         host = isinstance(x, np.ndarray)
         xd = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(self.device) if host else x
         bias = self._bias(reader, bias_name) if bias_name is not None and _has_tensor(reader, bias_name) else None
@@ -112,7 +155,7 @@ class GGUFGpuKernel:
         return y.cpu().numpy() if host else y
 
     def _bias(self, reader, name: str) -> torch.Tensor:
-        key = ("bias:" + name, 0)
+        key = ("bias", reader_key(reader), name)
         b = self._weights.get(key)
         if b is None:
             if isinstance(reader, GGUFFile):

@@ -94,3 +94,27 @@ def test_gemm_q4k_m2048_bias_via_linear():
     y = gguf_linear(x.cuda(), torch.from_numpy(blocks).cuda(), Q4_K, (1024, 2048), bias=b.cuda()).cpu().numpy()
     ref = matmul_ref.linear_ref(x.float().numpy(), w) + b.numpy()
     check_close(y, ref, "linear Q4_K m=2048")
+
+
+def test_gemm_q4k_small_magnitude_rows_via_linear():
+    """Every row is normalised by a power of two into float16's normal range,
+    so rows of tiny values keep full precision: rows at 1e-2 .. 1e-9 scale, one
+    row mixing magnitudes from 1e-9 to 1e3, a zero row and a row of bf16
+    subnormals, through gguf_linear (the workspace GEMM) at M > 16.  Each row is
+    held on its own to the 1e-3 bar against the fp64 oracle."""
+    n, k, m = 512, 1024, 40
+    blocks, w = quantized(Q4_K, n, k, 21)
+    x = activations(m, k, 21, torch.float32)
+    scales = {0: 1e-2, 1: 1e-4, 2: 1e-6, 3: 1e-9, 4: 1e-20, 5: 1e-30}
+    for r, sc in scales.items():
+        x[r] *= sc
+    x[6] *= torch.logspace(-9, 3, k)  # mixed magnitudes within one row
+    x[7] = 0.0
+    x[8] = torch.from_numpy(np.full(k, 2.0 ** -130, dtype=np.float32)) * torch.sign(x[8])  # bf16 subnormals
+    x = x.to(torch.bfloat16)
+    print("linear Q4_K small-magnitude rows m=40", flush=True)
+    y = gguf_linear(x.cuda(), torch.from_numpy(blocks).cuda(), Q4_K, (n, k)).cpu().numpy()
+    ref = matmul_ref.linear_ref(x.float().numpy(), w)
+    assert np.all(y[7] == 0.0), "zero row must give exact zeros"
+    for r in list(scales) + [6, 8, 9, 39]:
+        check_close(y[r], ref[r], f"linear Q4_K row {r}")

@@ -68,6 +68,11 @@ def test_linear_dispatch_large_m_float32():
     x = activations(37, 512, 9, torch.float32)
     y = gguf_linear(x.cuda(), torch.from_numpy(blocks).cuda(), Q8_0, (256, 512)).cpu().numpy()
     check_close(y, matmul_ref.linear_ref(x.numpy(), w), "linear f32 m=37")
+    # an odd N (a 32001-entry vocabulary, say): every 16-row tile's output stays 16-byte aligned
+    blocks, w = quantized(Q4_K, 1001, 512, 10)
+    x = activations(40, 512, 10, torch.float32)
+    y = gguf_linear(x.cuda(), torch.from_numpy(blocks).cuda(), Q4_K, (1001, 512)).cpu().numpy()
+    check_close(y, matmul_ref.linear_ref(x.numpy(), w), "linear f32 m=40 n=1001")
 
 
 def test_gemv_batched_decode_equals_sequential():

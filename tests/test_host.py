@@ -261,3 +261,44 @@ def test_decode_glue_validation_before_launch():
     assert call(32, 8, 128, 64, ws_bytes=16) == _native.DRACO_EWORKSPACE
     assert lib.draco_gguf_rms_norm(FAKE, FAKE, 1e-5, FAKE, None, 1, 6, None) == _native.DRACO_EINVAL_SHAPE
     assert lib.draco_gguf_rms_norm(FAKE, FAKE, 1e-5, None, None, 1, 8, None) == _native.DRACO_EINVAL_ARG
+
+
+def test_gpu_tier_cache_keys_separate_files_orders_and_bytes(tmp_path):
+    """Two files with the same tensor names and offsets but different bytes,
+    and one file read in both Q6_K field orders, never share a residency key;
+    neither do two matmul() calls handed different weight bytes."""
+    import time
+
+    from dracort_amd.format.gguf_file import GGUFFile
+    from dracort_amd.runtime.gpu_tier import bytes_weight_key, linear_weight_key
+    from tests.gguf_writer import write_gguf
+
+    rng = np.random.default_rng(3)
+    payloads = [rng.integers(0, 256, 210 * 4, dtype=np.uint8).tobytes() for _ in range(2)]
+    paths = []
+    for i, p in enumerate(payloads):
+        path = str(tmp_path / f"m{i}.gguf")
+        write_gguf(path, [("general.architecture", "str", "llama")], [("blk.0.ffn_down.weight", (4, 256), 14, p)])
+        paths.append(path)
+    keys = set()
+    for path in paths:
+        for order in ("reference", "ggml"):
+            with GGUFFile(path, field_order=order) as f:
+                t = f.tensor("blk.0.ffn_down.weight")
+                keys.add(linear_weight_key(f, t.info, t.kernel_type))
+    assert len(keys) == 4
+    # the same file reopened unchanged maps to the same key; rewritten, to a new one
+    with GGUFFile(paths[0]) as f:
+        t = f.tensor("blk.0.ffn_down.weight")
+        k0 = linear_weight_key(f, t.info, t.kernel_type)
+    with GGUFFile(paths[0]) as f:
+        assert linear_weight_key(f, t.info, t.kernel_type) == k0
+    time.sleep(0.01)
+    write_gguf(paths[0], [("general.architecture", "str", "llama")],
+               [("blk.0.ffn_down.weight", (4, 256), 14, payloads[1])])
+    with GGUFFile(paths[0]) as f:
+        assert linear_weight_key(f, f.tensor("blk.0.ffn_down.weight").info, 14) != k0
+    info = t.info
+    assert bytes_weight_key(info, 14, payloads[0]) != bytes_weight_key(info, 14, payloads[1])
+    assert bytes_weight_key(info, 14, payloads[0]) == bytes_weight_key(info, 14, bytes(payloads[0]))
+    assert bytes_weight_key(info, 14, payloads[0]) != bytes_weight_key(info, 14 | 0x100, payloads[0])

@@ -74,6 +74,11 @@ SIGNATURES = {
         [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_int, _c_i64, _vp, _vp, _vp, _c_int, _vp, _c_size,
          _vp],
     ),
+    "draco_gguf_dense_linear": (
+        _c_int, [_c_int, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_int, _vp]
+    ),
+    "draco_gguf_get_rows": (_c_int, [_c_int, _vp, _c_size, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp]),
+    "draco_gguf_swiglu": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -121,6 +121,16 @@ int draco_gguf_dequant_f32(int ggml_type, const void* blocks, size_t blocks_byte
   g_last_error[0] = 0;
   TypeInfo t;
   if (int rc = decode_type(ggml_type, &t)) return rc;
+  // Blocks may run across rows: the reference only needs n_rows * k to be a
+  // multiple of the block size (draco/format/gguf.py:292-296).  Such a
+  // tensor is one flat row of n_rows * k values (same output layout).
+  if (n_rows > 0 && k > 0 && n_rows <= kMaxDim && k <= kMaxDim && k % t.qk != 0 && (n_rows * k) % t.qk == 0) {
+    if (n_rows * k > kMaxDim)
+      return set_error(DRACO_EINVAL_SHAPE, "a tensor whose blocks run across rows holds at most %lld values",
+                       (long long)kMaxDim);
+    k *= n_rows;
+    n_rows = 1;
+  }
   if (int rc = check_matrix(t, n_rows, k)) return rc;
   if (int rc = check_bytes(t, n_rows, k, blocks_bytes, "blocks")) return rc;
   if (int rc = check_ptr(blocks, "blocks")) return rc;

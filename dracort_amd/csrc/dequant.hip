@@ -25,20 +25,33 @@
 
 namespace draco {
 
-__device__ __forceinline__ void st4(float* p, float a, float b, float c, float d) {
-  *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+// 16-byte store of four outputs; NaN in place of all four when `bad`.
+__device__ __forceinline__ void st4(float* p, float a, float b, float c, float d, bool bad) {
+  const float nan = __builtin_nanf("");
+  *reinterpret_cast<float4*>(p) = bad ? make_float4(nan, nan, nan, nan) : make_float4(a, b, c, d);
 }
 
+// Output row `row` holds weight row ids[row] (ids != NULL: the embedding
+// gather; an id outside [0, n_src_rows) gives a NaN row and reads row 0) or
+// weight row `row`.
 template <int QT, bool DL>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ w, float* __restrict__ out,
                                                       int64_t n_units, int units_per_row, int64_t row_bytes,
-                                                      int64_t k) {
+                                                      int64_t k, const int32_t* __restrict__ ids,
+                                                      int64_t n_src_rows) {
 #pragma clang fp contract(off)
   const int64_t gu = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gu >= n_units) return;
   const int64_t row = gu / units_per_row;
   const int u = (int)(gu - row * units_per_row);
-  const Raw<QT> r = load_unit<QT, DL>(w, row * row_bytes, u);
+  int64_t src = row;
+  bool bad = false;
+  if (ids) {
+    src = ids[row];
+    bad = src < 0 || src >= n_src_rows;
+    src = bad ? 0 : src;
+  }
+  const Raw<QT> r = load_unit<QT, DL>(w, src * row_bytes, u);
   float* o = out + row * k;
 
   if constexpr (QT == kQ8_0) {
@@ -47,7 +60,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       st4(p + 4 * j, sbyte_f(r.q[j], 0) * d, sbyte_f(r.q[j], 1) * d, sbyte_f(r.q[j], 2) * d,
-          sbyte_f(r.q[j], 3) * d);
+          sbyte_f(r.q[j], 3) * d, bad);
   } else if constexpr (QT == kQ4_0) {
     const float d = f16_bits_to_f32(r.d);
     float* p = o + group_pos<QT>(u, 0);
@@ -60,8 +73,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
         v[i] = (float)((int)((lo >> (8 * i)) & 0xFFu) - 8) * d;
         h[i] = (float)((int)((hi >> (8 * i)) & 0xFFu) - 8) * d;
       }
-      st4(p + 4 * j, v[0], v[1], v[2], v[3]);
-      st4(p + 16 + 4 * j, h[0], h[1], h[2], h[3]);
+      st4(p + 4 * j, v[0], v[1], v[2], v[3], bad);
+      st4(p + 16 + 4 * j, h[0], h[1], h[2], h[3], bad);
     }
   } else if constexpr (QT == kQ4_K) {
     const float d = f16_bits_to_f32(r.head.x), dmin = f16_bits_to_f32(r.head.x >> 16);
@@ -83,7 +96,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
           const float prod = d1 * ubyte_f(c, i);
           v[i] = prod - m1;
         }
-        st4(p + 4 * j, v[0], v[1], v[2], v[3]);
+        st4(p + 4 * j, v[0], v[1], v[2], v[3], bad);
       }
     }
   } else if constexpr (QT != kQ6_K) {
@@ -107,7 +120,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
           const float c = unit_code<QT>(r, g, 4 * j + i, u);
           v[i] = SYM ? (c - C) * a[g] : fmaf(a[g], c, b[g]);
         }
-        st4(p + 4 * j, v[0], v[1], v[2], v[3]);
+        st4(p + 4 * j, v[0], v[1], v[2], v[3], bad);
       }
     }
   } else {  // Q6_K
@@ -125,43 +138,49 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
         float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = dl * (float)((int)((c >> (8 * i)) & 0xFFu) - 32);
-        st4(p + 4 * h, v[0], v[1], v[2], v[3]);
+        st4(p + 4 * h, v[0], v[1], v[2], v[3], bad);
       }
     }
   }
 }
 
 template <int QT, bool DL>
-static int launch_dequant(const uint8_t* w, float* out, int64_t n_rows, int64_t k, hipStream_t s) {
+static int launch_dequant(const uint8_t* w, float* out, int64_t n_rows, int64_t k, const int32_t* ids,
+                          int64_t n_src_rows, hipStream_t s) {
   const int units_per_row = (int)(k / 32);
   const int64_t row_bytes = (k / Fmt<QT>::QK) * Fmt<QT>::BYTES;
   const int64_t n_units = n_rows * units_per_row;
   const int64_t blocks = (n_units + 255) / 256;
   hipLaunchKernelGGL((dequant_kernel<QT, DL>), dim3((unsigned)blocks), dim3(256), 0, s, w, out, n_units,
-                     units_per_row, row_bytes, k);
+                     units_per_row, row_bytes, k, ids, n_src_rows);
   return check_launch("dequant");
 }
 
 int dequant_dispatch(int qtype, bool d_last, const void* w, float* out, int64_t n_rows, int64_t k, hipStream_t s) {
+  return dequant_rows_dispatch(qtype, d_last, w, nullptr, n_rows, out, n_rows, k, s);
+}
+
+int dequant_rows_dispatch(int qtype, bool d_last, const void* w, const int32_t* ids, int64_t n_src_rows, float* out,
+                          int64_t n_rows, int64_t k, hipStream_t s) {
   const uint8_t* p = static_cast<const uint8_t*>(w);
   switch (qtype) {
-    case kQ8_0: return launch_dequant<kQ8_0, false>(p, out, n_rows, k, s);
-    case kQ4_0: return launch_dequant<kQ4_0, false>(p, out, n_rows, k, s);
-    case kQ4_1: return launch_dequant<kQ4_1, false>(p, out, n_rows, k, s);
-    case kQ5_0: return launch_dequant<kQ5_0, false>(p, out, n_rows, k, s);
-    case kQ5_1: return launch_dequant<kQ5_1, false>(p, out, n_rows, k, s);
-    case kQ8_K: return launch_dequant<kQ8_K, false>(p, out, n_rows, k, s);
-    case kQ4_K: return launch_dequant<kQ4_K, false>(p, out, n_rows, k, s);
-    case kQ5_K: return launch_dequant<kQ5_K, false>(p, out, n_rows, k, s);
+    case kQ8_0: return launch_dequant<kQ8_0, false>(p, out, n_rows, k, ids, n_src_rows, s);
+    case kQ4_0: return launch_dequant<kQ4_0, false>(p, out, n_rows, k, ids, n_src_rows, s);
+    case kQ4_1: return launch_dequant<kQ4_1, false>(p, out, n_rows, k, ids, n_src_rows, s);
+    case kQ5_0: return launch_dequant<kQ5_0, false>(p, out, n_rows, k, ids, n_src_rows, s);
+    case kQ5_1: return launch_dequant<kQ5_1, false>(p, out, n_rows, k, ids, n_src_rows, s);
+    case kQ8_K: return launch_dequant<kQ8_K, false>(p, out, n_rows, k, ids, n_src_rows, s);
+    case kQ4_K: return launch_dequant<kQ4_K, false>(p, out, n_rows, k, ids, n_src_rows, s);
+    case kQ5_K: return launch_dequant<kQ5_K, false>(p, out, n_rows, k, ids, n_src_rows, s);
     case kQ2_K:
-      return d_last ? launch_dequant<kQ2_K, true>(p, out, n_rows, k, s)
-                    : launch_dequant<kQ2_K, false>(p, out, n_rows, k, s);
+      return d_last ? launch_dequant<kQ2_K, true>(p, out, n_rows, k, ids, n_src_rows, s)
+                    : launch_dequant<kQ2_K, false>(p, out, n_rows, k, ids, n_src_rows, s);
     case kQ3_K:
-      return d_last ? launch_dequant<kQ3_K, true>(p, out, n_rows, k, s)
-                    : launch_dequant<kQ3_K, false>(p, out, n_rows, k, s);
+      return d_last ? launch_dequant<kQ3_K, true>(p, out, n_rows, k, ids, n_src_rows, s)
+                    : launch_dequant<kQ3_K, false>(p, out, n_rows, k, ids, n_src_rows, s);
     case kQ6_K:
-      return d_last ? launch_dequant<kQ6_K, true>(p, out, n_rows, k, s)
-                    : launch_dequant<kQ6_K, false>(p, out, n_rows, k, s);
+      return d_last ? launch_dequant<kQ6_K, true>(p, out, n_rows, k, ids, n_src_rows, s)
+                    : launch_dequant<kQ6_K, false>(p, out, n_rows, k, ids, n_src_rows, s);
     default: return set_error(DRACO_EINVAL_QTYPE, "unsupported ggml type %d", qtype);
   }
 }

@@ -18,6 +18,12 @@ int check_launch(const char* what);
 int dequant_dispatch(int qtype, bool d_last, const void* w, float* out, int64_t n_rows, int64_t k,
                      hipStream_t s);
 
+// Row gather with dequantization: out[i, :] = dequant(W[ids[i], :]) for
+// i < n_rows (ids NULL: row i itself); W has n_src_rows rows; an id outside
+// [0, n_src_rows) gives a NaN row.
+int dequant_rows_dispatch(int qtype, bool d_last, const void* w, const int32_t* ids, int64_t n_src_rows, float* out,
+                          int64_t n_rows, int64_t k, hipStream_t s);
+
 int gemv_dispatch(int qtype, bool d_last, const void* w, const void* x, bool x_bf16, const float* bias,
                   float* y, int m, int n, int k, hipStream_t s);
 

@@ -61,14 +61,6 @@ struct StreamJob {
   int64_t x_stride;
 };
 
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
-__device__ __forceinline__ float silu(float g) { return g / (1.f + __expf(-g)); }
-
 // Row r of this launch -> (matrix, row within it); rows of the matrices of a
 // kPlain launch are concatenated.
 __device__ __forceinline__ void row_of(const StreamJob& j, int r, int& mat, int& lrow) {

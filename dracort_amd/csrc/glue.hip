@@ -25,6 +25,14 @@
 //     a second launch, one workgroup per (sequence, query head), merges their
 //     partial states (max over the splits, rescaled sums) and writes the
 //     output.
+//
+// Shapes outside the fast kernels' set (head_dim other than 64 / 128, or a
+// query-head group other than 1, 2, 4 or 8: small test models, unusual GQA
+// ratios) run decode_attention_generic_kernel instead: one workgroup per
+// (query head, sequence) in three passes over the cached positions -- scores
+// into the workspace, exponentials and their sum, then the weighted value sum
+// -- with the same RoPE, float16 rounding of the new key / value and cache
+// store as the fast kernels.
 #include <math.h>
 
 #include "draco_internal.h"
@@ -429,7 +437,116 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(AttnArgs a) {
   }
 }
 
+__device__ __forceinline__ float block_max_256(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Any even head_dim D <= 256 and any group G = Hq / Hkv.  Workgroup (query
+// head qh, sequence b), 256 threads; a.part holds this workgroup's scores,
+// [B][Hq][max_pos] floats.  Every workgroup of kv head qh / G rotates the new
+// key itself (the same arithmetic as the fast kernel, so the same bits) and
+// uses it for position pos; the group's first query head stores k / v.
+__global__ __launch_bounds__(256) void decode_attention_generic_kernel(AttnArgs a, int D, int G) {
+  __shared__ float qs[256], kn[256], vn[256], acc[256];
+  __shared__ float red[4];
+  const int qh = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int h = qh / G, HALF = D / 2;
+  const int pos = a.positions[b];
+  const size_t at = (size_t)b * a.hq * D + (size_t)qh * D;
+  if (pos < 0 || pos >= a.max_pos) {  // no cache access; NaN output (uniform branch)
+    if (t < D) {
+      if (a.out_bf16)
+        static_cast<uint16_t*>(a.out)[at + t] = 0x7FC0u;
+      else
+        static_cast<float*>(a.out)[at + t] = __builtin_nanf("");
+    }
+    return;
+  }
+  const size_t head = ((size_t)b * a.hkv + h) * (size_t)a.max_pos * D;
+  if (t < HALF) {
+    const float c = a.cos_t ? a.cos_t[(size_t)pos * HALF + t] : 1.f;
+    const float sn = a.cos_t ? a.sin_t[(size_t)pos * HALF + t] : 0.f;
+    const float* qp = a.q + at;
+    const float q1 = qp[t], q2 = qp[t + HALF];
+    qs[t] = q1 * c - q2 * sn;
+    qs[t + HALF] = q2 * c + q1 * sn;
+    const float* kp = a.k + ((size_t)b * a.hkv + h) * D;
+    const float* vp = a.v + ((size_t)b * a.hkv + h) * D;
+    const float k1 = kp[t], k2 = kp[t + HALF];
+    const uint16_t kh1 = f32_to_f16(k1 * c - k2 * sn), kh2 = f32_to_f16(k2 * c + k1 * sn);
+    const uint16_t vh1 = f32_to_f16(vp[t]), vh2 = f32_to_f16(vp[t + HALF]);
+    kn[t] = f16_to_f32(kh1);
+    kn[t + HALF] = f16_to_f32(kh2);
+    vn[t] = f16_to_f32(vh1);
+    vn[t + HALF] = f16_to_f32(vh2);
+    if (qh % G == 0) {
+      a.kc[head + (size_t)pos * D + t] = kh1;
+      a.kc[head + (size_t)pos * D + t + HALF] = kh2;
+      a.vc[head + (size_t)pos * D + t] = vh1;
+      a.vc[head + (size_t)pos * D + t + HALF] = vh2;
+    }
+  }
+  __syncthreads();
+  float* sc = a.part + ((size_t)b * a.hq + qh) * (size_t)a.max_pos;
+  // 1. scores q . k / sqrt(D) of positions 0 .. pos
+  float mx = -INFINITY;
+  for (int j = t; j <= pos; j += 256) {
+    float sj = 0.f;
+    if (j == pos) {
+      for (int d = 0; d < D; ++d) sj = fmaf(qs[d], kn[d], sj);
+    } else {
+      const uint16_t* kr = a.kc + head + (size_t)j * D;
+      for (int d = 0; d < D; ++d) sj = fmaf(qs[d], f16_to_f32(kr[d]), sj);
+    }
+    sj *= a.scale;
+    sc[j] = sj;
+    mx = fmaxf(mx, sj);
+  }
+  mx = block_max_256(mx, red);
+  // 2. exponentials and their sum (each thread rewrites only its own scores)
+  float sum = 0.f;
+  for (int j = t; j <= pos; j += 256) {
+    const float e = expf(sc[j] - mx);
+    sc[j] = e;
+    sum += e;
+  }
+  sum = block_sum_256(sum, red);  // its barriers also order the score writes before pass 3
+  // 3. weighted value sums: thread group g = t / D takes positions g, g + NG, ...
+  const int NG = 256 / D, g = t / D, d = t - g * D;
+  float o = 0.f;
+  if (g < NG) {
+    for (int j = g; j <= pos; j += NG) {
+      const float vj = j == pos ? vn[d] : f16_to_f32(a.vc[head + (size_t)j * D + d]);
+      o = fmaf(sc[j], vj, o);
+    }
+  }
+  acc[t] = o;
+  __syncthreads();
+  if (t < D) {
+    float tot = 0.f;
+    for (int gg = 0; gg < NG; ++gg) tot += acc[gg * D + t];
+    const float r = tot / sum;
+    if (a.out_bf16)
+      static_cast<uint16_t*>(a.out)[at + t] = f32_to_bf16_bits(r);
+    else
+      static_cast<float*>(a.out)[at + t] = r;
+  }
+}
+
+// The fast kernels take head_dim 64 / 128 with 1, 2, 4 or 8 query heads per kv head.
+inline bool attn_fast_shape(int hq, int hkv, int head_dim) {
+  const int g = hq / hkv;
+  return (head_dim == 64 || head_dim == 128) && g <= kMaxGroup && (g & (g - 1)) == 0;
+}
+
 size_t decode_attention_ws(int64_t batch, int hq, int hkv, int head_dim, int64_t max_pos) {
+  if (!attn_fast_shape(hq, hkv, head_dim)) return (size_t)batch * hq * max_pos * sizeof(float);
   const AttnSplit sp = attn_split(max_pos);
   return (size_t)batch * hkv * sp.splits * (hq / hkv) * (head_dim + 4) * sizeof(float);
 }
@@ -457,8 +574,13 @@ int decode_attention_launch(const float* q, const float* k, const float* v, uint
   a.sin_t = sin_t;
   a.scale = (float)(1.0 / sqrt((double)head_dim));
   a.out_bf16 = out_bf16;
-  const dim3 grid((unsigned)a.splits, (unsigned)hkv, (unsigned)batch);
   const int g = hq / hkv;
+  if (!attn_fast_shape(hq, hkv, head_dim)) {
+    hipLaunchKernelGGL(decode_attention_generic_kernel, dim3((unsigned)hq, (unsigned)batch), dim3(256), 0, s, a,
+                       head_dim, g);
+    return check_launch("decode_attention_generic");
+  }
+  const dim3 grid((unsigned)a.splits, (unsigned)hkv, (unsigned)batch);
   const dim3 mgrid((unsigned)hq, (unsigned)batch);
 #define DRACO_ATTN_LAUNCH(D_, G_)                                                                \
   hipLaunchKernelGGL((decode_attention_kernel<D_, G_>), grid, dim3(64), 0, s, a);               \
@@ -517,15 +639,14 @@ int draco_gguf_decode_attention(const float* q, const float* k, const float* v, 
                                 const int32_t* positions, int64_t batch, int n_q_heads, int n_kv_heads, int head_dim,
                                 int64_t max_positions, const float* rope_cos, const float* rope_sin, void* out,
                                 int out_dtype, void* workspace, size_t workspace_bytes, void* stream) {
-  if (batch < 1 || batch > 65535 || n_kv_heads < 1 || n_kv_heads > 65535 || n_q_heads < n_kv_heads ||
-      n_q_heads % n_kv_heads || n_q_heads / n_kv_heads > kMaxGroup ||
-      ((n_q_heads / n_kv_heads) & (n_q_heads / n_kv_heads - 1)))
+  if (batch < 1 || batch > 65535 || n_kv_heads < 1 || n_q_heads > 65535 || n_q_heads < n_kv_heads ||
+      n_q_heads % n_kv_heads)
     return set_error(DRACO_EINVAL_SHAPE,
-                     "decode attention needs 1 <= batch <= 65535, n_q_heads = 1, 2, 4 or 8 (<= %d) x n_kv_heads; got "
-                     "batch %lld, %d / %d heads",
-                     kMaxGroup, (long long)batch, n_q_heads, n_kv_heads);
-  if (head_dim != 64 && head_dim != 128)
-    return set_error(DRACO_EINVAL_SHAPE, "decode attention takes head_dim 64 or 128, got %d", head_dim);
+                     "decode attention needs 1 <= batch <= 65535 and n_q_heads (<= 65535) a multiple of n_kv_heads; "
+                     "got batch %lld, %d / %d heads",
+                     (long long)batch, n_q_heads, n_kv_heads);
+  if (head_dim < 2 || head_dim > 256 || head_dim % 2)
+    return set_error(DRACO_EINVAL_SHAPE, "decode attention takes an even head_dim of 2..256, got %d", head_dim);
   if (max_positions < 1 || max_positions * head_dim * (int64_t)n_kv_heads * batch > ((int64_t)1 << 40) ||
       max_positions > kMaxPositions)
     return set_error(DRACO_EINVAL_SHAPE, "invalid max_positions %lld", (long long)max_positions);

@@ -1,5 +1,6 @@
 """GPU operators of the GGUF quantized-matmul path (HIP kernels, gfx950)."""
 
+from dracort_amd.kernels.dense import dense_linear, get_rows, swiglu  # noqa: F401
 from dracort_amd.kernels.glue import (  # noqa: F401
     DecodeAttentionWorkspace,
     decode_attention,
@@ -42,4 +43,7 @@ __all__ = [
     "decode_attention_workspace_bytes",
     "DecodeAttentionWorkspace",
     "rope_tables",
+    "dense_linear",
+    "get_rows",
+    "swiglu",
 ]

@@ -79,11 +79,30 @@ def _x_dtype(x: torch.Tensor) -> int:
     raise ValueError(f"activations must be float32 or bfloat16, got {x.dtype}")
 
 
+def _flat_bytes(ggml_type: int, n: int, k: int) -> int:
+    """Bytes of an [n, k] tensor whose blocks may run across rows (the
+    reference's rule: n * k a multiple of the block size)."""
+    qk, nb = layout(ggml_type)
+    if (n * k) % qk:
+        raise DracoFormatError(
+            f"GGUF tensor [{n}, {k}] has {n * k} elements, not a multiple of block size {qk} for ggml type {ggml_type}"
+        )
+    return n * k // qk * nb
+
+
 def gguf_dequantize(
     qweight: torch.Tensor, ggml_type: int, shape: Tuple[int, int], out: Optional[torch.Tensor] = None
 ) -> torch.Tensor:
-    """float32 [N, K] weight, bit-exact to the reference dequantization."""
-    n, k = _check_weight(qweight, ggml_type, shape)
+    """float32 [N, K] weight, bit-exact to the reference dequantization.  K
+    need not be a multiple of the block size when N * K is (blocks running
+    across rows, as ``_dequantize`` allows, ``draco/format/gguf.py:292-296``)."""
+    n, k = int(shape[0]), int(shape[1])
+    if len(shape) == 2 and k % layout(ggml_type)[0] != 0:
+        _need_gpu(qweight, "qweight")
+        if qweight.dtype != torch.uint8 or qweight.numel() < _flat_bytes(ggml_type, n, k):
+            raise DracoFormatError(f"GGUF payload holds {qweight.numel()} bytes, too few for {tuple(shape)}")
+    else:
+        n, k = _check_weight(qweight, ggml_type, shape)
     if out is None:
         out = torch.empty((n, k), dtype=torch.float32, device=qweight.device)
     else:

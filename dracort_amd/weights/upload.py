@@ -9,10 +9,11 @@ in chunks into two pinned host buffers that alternate, each chunk copied to
 the device asynchronously on a dedicated stream while the next is being
 filled, so disk / page-cache reads overlap the host-to-device copies.
 
-Quantized 2-D tensors of a type the kernels run (Q8_0, Q4_0, Q4_K, Q6_K)
-come back as :class:`GGUFQuantizedWeight`; float tensors (norms, embeddings)
-as device tensors of their dtype and shape; any other block type as its raw
-uint8 bytes.
+Quantized 2-D tensors of a block type the kernels run, with whole blocks
+per row, come back as :class:`GGUFQuantizedWeight`; float tensors (norms,
+embeddings) as device tensors of their dtype and shape; everything else
+(3-D expert stacks, tensors whose blocks run across rows) as raw uint8
+bytes.
 """
 
 from __future__ import annotations
@@ -86,7 +87,8 @@ def upload_gguf(
         ttype = t.info.ggml_type
         if ttype in FLOAT_TYPES:
             out[name] = dst.view(_TORCH_FLOAT[FLOAT_TYPES[ttype][0]]).reshape(t.shape)
-        elif base_type(t.kernel_type) in BLOCK_LAYOUTS and len(t.shape) == 2:
+        elif (base_type(t.kernel_type) in BLOCK_LAYOUTS and len(t.shape) == 2
+              and t.shape[1] % BLOCK_LAYOUTS[base_type(t.kernel_type)][0] == 0):
             out[name] = GGUFQuantizedWeight(dst, t.kernel_type, t.shape)
         else:
             out[name] = dst

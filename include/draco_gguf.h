@@ -82,7 +82,9 @@ int draco_gguf_block_info(int ggml_type, int* qk, int* block_bytes);
 
 /*
  * out[n_rows, k] (float32) = dequantize(blocks), bit-exact to the reference
- * float32 dequant.  Replaces _dequantize(qtype, payload, n)
+ * float32 dequant.  Blocks may run across rows when k is not a multiple of
+ * the block size, as long as n_rows * k is (the reference's rule, at most
+ * 2^30 values in that case).  Replaces _dequantize(qtype, payload, n)
  * (draco/format/gguf.py:272-497) as called by GGUFReader.get_tensor
  * (draco/format/gguf.py:820-834).
  */
@@ -234,9 +236,12 @@ size_t draco_gguf_decode_attention_workspace_size(int64_t batch, int n_q_heads, 
  * position, and write the attention of q over positions 0 .. p of its
  * sequence (query head h reads kv head h / (n_q_heads / n_kv_heads);
  * scores q.k / sqrt(head_dim), softmax, weighted sum of v) to out
- * [b, n_q_heads * head_dim], float32 or bfloat16 (out_dtype).  head_dim 64
- * or 128, 1, 2, 4 or 8 query heads per kv head, max_positions <= 131072.
- * Two launches: partial attention per 256-position split, then the merge.
+ * [b, n_q_heads * head_dim], float32 or bfloat16 (out_dtype).  Any even
+ * head_dim of 2..256, n_q_heads a multiple of n_kv_heads, max_positions <=
+ * 131072.  head_dim 64 or 128 with 1, 2, 4 or 8 query heads per kv head run
+ * two launches (partial attention per position split, then the merge); other
+ * shapes one workgroup per (query head, sequence) whose workspace holds the
+ * scores (draco_gguf_decode_attention_workspace_size gives either size).
  * A position outside [0, max_positions) touches no cache memory and yields
  * NaN outputs.
  * Replaces apply_rope (draco/runtime/cpu/ops.py:73-92) on q / k and
@@ -247,6 +252,41 @@ int draco_gguf_decode_attention(const float* q, const float* k, const float* v, 
                                 const int32_t* positions, int64_t batch, int n_q_heads, int n_kv_heads, int head_dim,
                                 int64_t max_positions, const float* rope_cos, const float* rope_sin, void* out,
                                 int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Executor pieces for the tensors of a GGUF model that are not
+ * block-quantized, and the glue between projections that were not fused.
+ *
+ * draco_gguf_dense_linear: y[m, n] = x[m, k] . W[n, k]^T (+ bias[n]) for a
+ * float weight, ggml_type F32 (0), F16 (1) or BF16 (30); x float32 or
+ * bfloat16 (x_dtype), float32 accumulation; accumulate != 0 adds the result
+ * into y (the residual add).  Replaces _linear on a tensor with
+ * quantization=None: get_tensor(dequantize=True) then matmul_f32
+ * (draco/runtime/cpu/executor.py:47-52, 77-78,
+ * draco/runtime/cpu/kernels/generic.py:32-33).
+ */
+int draco_gguf_dense_linear(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype,
+                            const float* bias, float* y, int64_t m, int64_t n, int64_t k, int accumulate,
+                            void* stream);
+
+/*
+ * Embedding gather: out[i, :] (float32) = row ids[i] of the [n_rows, k]
+ * table w, for i < n_ids (<= 65535); ids are device int32.  Block-quantized
+ * tables (k a multiple of the block size) are dequantized bit-exactly as
+ * draco_gguf_dequant_f32 does; F32 / F16 / BF16 tables are converted.  An id
+ * outside [0, n_rows) gives a row of NaN.  Replaces embed[token_ids] after
+ * get_tensor(embed_name, dequantize=True) in _initial_hidden
+ * (draco/runtime/cpu/executor.py:279-288).
+ */
+int draco_gguf_get_rows(int ggml_type, const void* w, size_t w_bytes, int64_t n_rows, int64_t k, const int32_t* ids,
+                        int64_t n_ids, float* out, void* stream);
+
+/*
+ * y = silu(gate) * up over n float32 values into float32 y and / or bfloat16
+ * y_bf16 (either may be NULL, not both): swiglu (draco/runtime/cpu/ops.py:19-27)
+ * for gate / up projections computed by separate launches.
+ */
+int draco_gguf_swiglu(const float* gate, const float* up, float* y, void* y_bf16, int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

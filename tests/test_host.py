@@ -254,8 +254,12 @@ def test_decode_glue_validation_before_launch():
     def call(hq, hkv, d, max_pos, ws_bytes=1 << 30, cos=None, sin=None):
         return lib.draco_gguf_decode_attention(args["q"], args["k"], args["v"], args["kc"], args["vc"], args["pos"],
                                                1, hq, hkv, d, max_pos, cos, sin, FAKE, 0, FAKE, ws_bytes, None)
-    assert call(12, 4, 128, 64) == _native.DRACO_EINVAL_SHAPE     # 3 query heads per kv head
-    assert call(32, 8, 96, 64) == _native.DRACO_EINVAL_SHAPE      # head_dim
+    assert call(12, 8, 128, 64) == _native.DRACO_EINVAL_SHAPE     # query heads not a multiple of kv heads
+    assert call(32, 8, 97, 64) == _native.DRACO_EINVAL_SHAPE      # odd head_dim
+    assert call(32, 8, 258, 64) == _native.DRACO_EINVAL_SHAPE     # head_dim above 256
+    # other head_dims and groups run the generic kernel, whose workspace holds the scores
+    assert lib.draco_gguf_decode_attention_workspace_size(2, 12, 4, 96, 1000) == 2 * 12 * 1000 * 4
+    assert lib.draco_gguf_decode_attention_workspace_size(1, 4, 2, 4, 64) == 4 * 64 * 4
     assert call(32, 8, 128, 1 << 25) == _native.DRACO_EINVAL_SHAPE
     assert call(32, 8, 128, 64, cos=FAKE) == _native.DRACO_EINVAL_ARG
     assert call(32, 8, 128, 64, ws_bytes=16) == _native.DRACO_EWORKSPACE

@@ -27,12 +27,13 @@ Two forms of the step:
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import Dict, List, Optional
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
 from dracort_amd.exceptions import KVCacheError
 from dracort_amd.format.gguf import GGML_TYPE_Q4_K, GGML_TYPE_Q6_K, tensor_bytes
+from dracort_amd.kernels.dense import get_rows
 from dracort_amd.kernels.glue import DecodeAttentionWorkspace, decode_attention, rms_norm, rope_tables
 from dracort_amd.kernels.gguf import (
     gguf_gemv,
@@ -88,6 +89,8 @@ class LayerSet:
     # float32 RMSNorm weights per layer ("attn", "ffn") and the final one
     norms: List[Dict[str, torch.Tensor]] = field(default_factory=list)
     output_norm: Optional[torch.Tensor] = None
+    # token embedding table (raw bytes on the device, its ggml type and [vocab, hidden] shape), if any
+    embed: Optional[Tuple[torch.Tensor, int, Tuple[int, int]]] = None
 
     @property
     def weight_bytes(self) -> int:
@@ -123,6 +126,74 @@ def synthetic_layer_set(shape: LlamaShape, seed: int = 0, device="cuda", types=N
                          for p in ("attn", "ffn")})
     ls.output_norm = 1.0 + 0.1 * torch.randn(shape.hidden, generator=gen, device=device)
     return ls
+
+
+def layer_set_from_gguf(reader, device="cuda", max_positions: Optional[int] = None):
+    """(LayerSet, AttentionShape) of a dense llama-family GGUF file for the
+    fused decode step: the tensor names and metadata the reference's
+    ``_build_index`` / ``_build_metadata`` read (``draco/format/gguf.py:604-772``)
+    and ``CPUExecutorConfig.from_metadata`` consumes
+    (``draco/runtime/cpu/executor.py:108-129``), every projection uploaded in
+    its packed layout, the token embedding table kept for the gather.  The
+    step's fused launches need block-quantized q/k/v/o/gate/up/down and
+    lm_head with whole blocks per row, gate and up of one type, no biases and
+    no experts; other files run on :class:`GPUExecutionBackend`."""
+    from dracort_amd.format.gguf import BLOCK_LAYOUTS, base_type
+    from dracort_amd.runtime.executor import gguf_executor_config
+    from dracort_amd.weights.upload import upload_gguf
+
+    cfg = gguf_executor_config(reader)
+    if cfg.num_experts or cfg.qkv_fused or cfg.attention_bias or cfg.mlp_bias:
+        raise ValueError("the fused decode step takes dense models with separate, bias-free q/k/v projections")
+    hd = cfg.head_dim
+    names = ["token_embd.weight", "output_norm.weight"] + ([] if cfg.tie_word_embeddings else ["output.weight"])
+    gg = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate", "up": "ffn_up",
+          "down": "ffn_down"}
+    for i in range(cfg.num_hidden_layers):
+        names += [f"blk.{i}.{gg[p]}.weight" for p in PROJ] + [f"blk.{i}.attn_norm.weight", f"blk.{i}.ffn_norm.weight"]
+    up = upload_gguf(reader, names, device=device)
+
+    def block(name):
+        w = up[name]
+        if not isinstance(w, GGUFQuantizedWeight):
+            raise ValueError(f"'{name}' is not a block-quantized tensor with whole blocks per row")
+        return w
+
+    def f32(name):
+        t = up[name]
+        if not isinstance(t, torch.Tensor) or not t.is_floating_point():
+            raise ValueError(f"'{name}' must be a float tensor")
+        return t.to(torch.float32).reshape(-1).contiguous()
+
+    inter = cfg.intermediate_size or reader.tensor("blk.0.ffn_gate.weight").shape[0]
+    shape = LlamaShape(hidden=cfg.hidden_size, inter=inter, kv_dim=cfg.num_key_value_heads * hd,
+                       vocab=cfg.vocab_size, n_layers=cfg.num_hidden_layers)
+    ls = LayerSet(shape)
+    for i in range(cfg.num_hidden_layers):
+        layer = {p: block(f"blk.{i}.{gg[p]}.weight") for p in PROJ}
+        if layer["gate"].ggml_type != layer["up"].ggml_type:
+            raise ValueError(f"layer {i}: gate and up projections of different types")
+        for p in PROJ:
+            if tuple(layer[p].shape) != shape.proj_shape(p):
+                raise ValueError(f"layer {i} {p}: shape {layer[p].shape}, expected {shape.proj_shape(p)}")
+        ls.layers.append(layer)
+        ls.norms.append({"attn": f32(f"blk.{i}.attn_norm.weight"), "ffn": f32(f"blk.{i}.ffn_norm.weight")})
+    ls.output_norm = f32("output_norm.weight")
+    et = reader.tensor("token_embd.weight")
+    e = up["token_embd.weight"]
+    edata = e.data if isinstance(e, GGUFQuantizedWeight) else e.reshape(-1).view(torch.uint8)
+    ekind = e.ggml_type if isinstance(e, GGUFQuantizedWeight) else et.info.ggml_type
+    ls.embed = (edata, ekind, tuple(et.shape))
+    if cfg.tie_word_embeddings:
+        if not isinstance(e, GGUFQuantizedWeight) or base_type(e.ggml_type) not in BLOCK_LAYOUTS:
+            raise ValueError("tied embeddings must be block-quantized for the fused decode step's lm_head")
+        ls.lm_head = e
+    else:
+        ls.lm_head = block("output.weight")
+    attn = AttentionShape(n_heads=cfg.num_attention_heads, n_kv_heads=cfg.num_key_value_heads, head_dim=hd,
+                          rope_theta=cfg.rope_theta, rms_eps=cfg.rms_norm_eps,
+                          max_positions=int(max_positions or cfg.max_position_embeddings))
+    return ls, attn
 
 
 def layer_set_bytes(shape: LlamaShape, types=None, lm_head_type: int = GGML_TYPE_Q6_K) -> int:
@@ -177,6 +248,31 @@ class DecodeStep:
             self.vf = torch.empty((m, s.kv_dim), **f32)
             self.xn = torch.empty((m, s.hidden), **b16)
             self.att = torch.empty((m, s.hidden), **b16)
+        # token input through the embedding gather (set_tokens); otherwise x_in
+        self.ids = torch.zeros((m,), dtype=torch.int32, device=device) if ls.embed is not None else None
+        self.use_tokens = False
+
+    def set_tokens(self, ids) -> None:
+        """The next step's input tokens (one per sequence): their embedding rows
+        replace x_in.  The ids buffer is updated in place, so a captured graph
+        picks them up on its next replay."""
+        if self.ids is None:
+            raise ValueError("the layer set carries no embedding table")
+        t = torch.as_tensor(ids, dtype=torch.int32).reshape(-1)
+        if t.numel() != self.m:
+            raise ValueError(f"need {self.m} token ids, got {t.numel()}")
+        vocab = self.ls.embed[2][0]
+        if int(t.min()) < 0 or int(t.max()) >= vocab:
+            raise ValueError(f"token ids must be in [0, {vocab})")
+        self.ids.copy_(t.to(self.ids.device))
+        self.use_tokens = True
+
+    def _input(self) -> None:
+        if self.use_tokens:
+            table, gt, shp = self.ls.embed
+            get_rows(table, gt, shp, self.ids, out=self.h)
+        else:
+            self.h.copy_(self.x_in)
 
     def run(self) -> torch.Tensor:
         if self.attn is not None:
@@ -209,7 +305,7 @@ class DecodeStep:
     def _run_full(self) -> torch.Tensor:
         s, a = self.ls.shape, self.attn
         self._claim_position()
-        self.h.copy_(self.x_in)
+        self._input()
         for li, layer in enumerate(self.ls.layers):
             norms = self.ls.norms[li]
             q, k, v, o = layer["q"], layer["k"], layer["v"], layer["o"]

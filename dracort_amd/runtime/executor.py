@@ -367,7 +367,10 @@ class GPUExecutionBackend:
         f32 = dict(dtype=torch.float32, device=dev)
         hd, hq, hkv = cfg.head_dim, cfg.num_attention_heads, cfg.num_key_value_heads
         ids = torch.tensor(tokens, dtype=torch.int32, device=dev)
-        pos = torch.tensor(positions, dtype=torch.int32, device=dev)
+        # one 16-byte row per sequence: each sequence's position is its own aligned [1] view
+        pos = torch.zeros((m, 4), dtype=torch.int32)
+        pos[:, 0] = torch.tensor(positions, dtype=torch.int32)
+        pos = pos.to(dev)
         h = torch.empty((m, cfg.hidden_size), **f32)
         get_rows(self.embed.data, self.embed.ggml_type, self.embed.shape, ids, out=h)
         xn = torch.empty_like(h)
@@ -378,7 +381,7 @@ class GPUExecutionBackend:
             for i, s in enumerate(seq_ids):
                 slot = self._slots[s]
                 decode_attention(q[i:i + 1], k[i:i + 1], v[i:i + 1], self.k_cache[li][slot:slot + 1],
-                                 self.v_cache[li][slot:slot + 1], pos[i:i + 1], hq, hkv, rope=self.rope,
+                                 self.v_cache[li][slot:slot + 1], pos[i, :1], hq, hkv, rope=self.rope,
                                  out=att[i:i + 1], workspace=self.attn_ws)
             self._linear(L.o, att, h, bias=L.bias.get("attn_output"), accumulate=True)
             rms_norm(h, L.ffn_norm, cfg.rms_norm_eps, out=xn)

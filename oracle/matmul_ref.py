@@ -8,6 +8,10 @@
                      ``_linear`` (``draco/runtime/cpu/executor.py:47-79``).
 * ``cpu_linear_f32`` exactly the reference's float32 numpy expression; this is
                      the timed CPU baseline, not a checker.
+* ``cpu_moe_f32``    the reference's MoE in float32 (top-k of the logits,
+                     softmax, per-expert ``F.linear`` SwiGLU FFN on the tokens
+                     routed to it, weighted sum) with numpy/OpenBLAS: the timed
+                     CPU baseline of the MoE configuration, not a checker.
 * ``moe_ref``        top-k router (``draco/models/moe/router.py:81-120``: topk of
                      the logits, softmax over the k selected logits, renormalise)
                      and the expert loop (``draco/models/moe/expert.py:77-116``:
@@ -89,4 +93,21 @@ def moe_ref(
         ye = h @ np.asarray(wd, np.float64).T
         we = (w[hit] * (idx[hit] == e)).sum(axis=1, keepdims=True)
         out[hit] += ye * we
+    return out
+
+
+def cpu_moe_f32(x: np.ndarray, logits: np.ndarray, experts, top_k: int) -> np.ndarray:
+    """float32 MoE FFN as the reference's modules compute it on the CPU (timed baseline)."""
+    x32 = np.asarray(x, dtype=np.float32)
+    idx, w = route_ref(logits, top_k)
+    out = np.zeros_like(x32)
+    for e, (wg, wu, wd) in enumerate(experts):
+        hit = np.nonzero((idx == e).any(axis=1))[0]
+        if hit.size == 0:
+            continue
+        xe = x32[hit]
+        g = xe @ wg.T
+        h = g / (1.0 + np.exp(-g)) * (xe @ wu.T)
+        we = (w[hit] * (idx[hit] == e)).sum(axis=1, keepdims=True).astype(np.float32)
+        out[hit] += (h @ wd.T) * we
     return out

@@ -29,6 +29,7 @@ DRACO_DTYPE_F32 = 0
 DRACO_DTYPE_BF16 = 1
 DRACO_GGUF_GGML_ORDER = 0x100  # Q2_K / Q3_K / Q6_K in upstream ggml field order
 DRACO_GGUF_Q6K_D_LAST = DRACO_GGUF_GGML_ORDER
+DRACO_GGUF_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 ABI_VERSION = 3
 
@@ -52,6 +53,9 @@ SIGNATURES = {
     "draco_gguf_gemm": (_c_int, [_c_int, _vp, _c_size, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_size, _vp]),
     "draco_gguf_linear": (
         _c_int, [_c_int, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_size, _vp]
+    ),
+    "draco_gguf_linear_noalloc": (
+        _c_int, [_c_int, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]
     ),
     "draco_gguf_moe_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "draco_gguf_moe_ffn": (

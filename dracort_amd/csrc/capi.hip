@@ -4,6 +4,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "draco_internal.h"
 #include "gguf_common.h"
 
@@ -94,6 +96,37 @@ bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
 int check_ptr(const void* p, const char* name) {
   if (p == nullptr) return set_error(DRACO_EINVAL_ARG, "%s is NULL", name);
   if (!aligned16(p)) return set_error(DRACO_EINVAL_ARG, "%s is not 16-byte aligned", name);
+  return DRACO_OK;
+}
+
+// Scratch of draco_gguf_linear_noalloc: the Q4_K prefill GEMM's workspace
+// (float16 activations, sub-block sums, row scales) for callers that cannot
+// allocate.  One copy per GPU the library runs on, held until the process
+// ends.  Host code never passes `scratch` itself (in host code it names a
+// host-side stand-in): it takes each device's address from
+// hipGetSymbolAddress once, with that device current, and passes that.
+static __device__ __align__(256) unsigned char scratch[DRACO_GGUF_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 256;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];
+
+// The current device's scratch address (looked up on the first call on that device).
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(DRACO_EHIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices) return set_error(DRACO_EHIP, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(DRACO_EHIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                       e != hipSuccess ? hipGetErrorString(e) : "NULL address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
   return DRACO_OK;
 }
 
@@ -362,6 +395,30 @@ int draco_gguf_linear(int ggml_type, const void* w, size_t w_bytes, const void* 
     if (rc) return rc;
   }
   return DRACO_OK;
+}
+
+int draco_gguf_linear_noalloc(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype,
+                              const float* bias, float* y, int64_t m, int64_t n, int64_t k, void* stream) {
+  g_last_error[0] = 0;
+  // the GEMV (m <= 16) and the float32 16-row tiles use no workspace
+  if ((m >= 1 && m <= 16) || x_dtype != DRACO_DTYPE_BF16)
+    return draco_gguf_linear(ggml_type, w, w_bytes, x, x_dtype, bias, y, m, n, k, nullptr, 0, stream);
+  TypeInfo t;
+  if (int rc = decode_type(ggml_type, &t)) return rc;
+  if (m < 1 || m > kMaxDim || k < 1 || k > kMaxDim)
+    return set_error(DRACO_EINVAL_SHAPE, "invalid token count %lld or row length %lld", (long long)m, (long long)k);
+  const size_t need = gemm_workspace_size(t.base, m, k);
+  if (need == 0)  // this type's GEMM needs no workspace
+    return draco_gguf_gemm(ggml_type, w, w_bytes, x, bias, y, m, n, k, nullptr, 0, stream);
+  if (need > (size_t)DRACO_GGUF_NOALLOC_SCRATCH_BYTES)
+    return set_error(DRACO_EWORKSPACE,
+                     "draco_gguf_linear_noalloc: %lld rows of length %lld need %zu bytes of scratch, above its %zu-byte "
+                     "maximum (split the rows, or call draco_gguf_linear with a workspace)",
+                     (long long)m, (long long)k, need, (size_t)DRACO_GGUF_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (int rc = scratch_for_current_device(&ws)) return rc;
+  return draco_gguf_gemm(ggml_type, w, w_bytes, x, bias, y, m, n, k, ws, (size_t)DRACO_GGUF_NOALLOC_SCRATCH_BYTES,
+                         stream);
 }
 
 }  // extern "C"

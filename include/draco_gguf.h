@@ -170,6 +170,26 @@ int draco_gguf_linear(int ggml_type, const void* w, size_t w_bytes, const void* 
                       void* stream);
 
 /*
+ * draco_gguf_linear that allocates nothing and takes no workspace.  No
+ * counterpart in the reference: this entry point is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The Q4_K prefill GEMM's workspace lives
+ * in a static device array of DRACO_GGUF_NOALLOC_SCRATCH_BYTES per GPU (held
+ * by each GPU the library runs on until the process ends), enough for
+ * m = 2048 rows of k = 14336; a call needing more (see
+ * draco_gguf_gemm_workspace_size) fails with DRACO_EWORKSPACE before any
+ * launch.  The array of the calling thread's current device is used, so the
+ * stream must belong to that device; its address is looked up on the first
+ * call on each device (make that first call outside graph capture).  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (concurrent streams, threads or processes' graphs replayed together) race.
+ * Nothing in the array needs to start at zero (each call writes what it reads).
+ */
+#define DRACO_GGUF_NOALLOC_SCRATCH_BYTES (64u << 20)
+int draco_gguf_linear_noalloc(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype,
+                              const float* bias, float* y, int64_t m, int64_t n, int64_t k, void* stream);
+
+/*
  * Workspace bytes draco_gguf_moe_ffn needs for `tokens` tokens.
  */
 size_t draco_gguf_moe_workspace_size(int64_t tokens, int64_t hidden, int64_t inter, int n_experts, int top_k);

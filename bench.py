@@ -21,6 +21,11 @@ Printed (one JSON line on stdout):
   cpu_baseline  the reference CPU path (numpy dequant + float32 x @ W.T,
              as the oracle restates it) on the host cores, warm fp32-weight
              cache, one layer + 1/8 of lm_head timed and scaled to a step
+  configs    configurations 1, 2, 4 and 5 at full size on the GPU, each with
+             the reference CPU path timed beside it (warm, cold, one thread)
+  full_decode  the complete decode step (norms, RoPE, KV cache, attention)
+Modes: --stream-probe (read-only kernel at each launch size: the per-launch
+ceiling), --suite / --types / --traffic-probe / --mfma-probe / --moe-probe.
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
 
@@ -420,6 +425,222 @@ def moe_probe(reps: int):
     log(f"moe probe: x{reps}")
 
 
+PROBE_LIB = os.path.join(ROOT, "dracort_amd", "lib", "libdraco_probe.so")
+
+
+def stream_probe(reps: int):
+    """The single-launch ceiling: a kernel that only reads (16-byte loads,
+    four in flight per thread) one buffer of each decode-step launch size,
+    timed like the roofline kernel (HIP events around graph replays of a
+    rotation of distinct buffers beyond the Infinity Cache), over several grid
+    sizes.  One JSON line per (size, grid) and one summary line per size."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(PROBE_LIB)
+    lib.draco_probe_stream_read.restype = ctypes.c_int
+    lib.draco_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
+                                            ctypes.c_void_p]
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    sizes = {"o 4096x4096 Q4_K": 9437184, "q/k/v 6144x4096 Q4_K": 14155776, "gate 14336x4096 Q4_K": 33030144,
+             "down 4096x14336 Q6_K": 48168960, "gate+up 2x14336x4096 Q4_K": 66060288}
+    lines = []
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for what, nbytes in sizes.items():
+        bufs = rotation(lambda: torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_(0, 255), nbytes)
+        best = None
+        for per_cu in (1, 2, 4, 8):
+            blocks = cus * per_cu
+
+            def launch(b=None, blocks=blocks):
+                rc = lib.draco_probe_stream_read(b.data_ptr(), nbytes, blocks, sink.data_ptr(),
+                                                 torch.cuda.current_stream().cuda_stream)
+                assert rc == 0, rc
+
+            ms = time_launches([lambda b=b: launch(b) for b in bufs], reps)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            line = {"probe": "stream_read", "launch": what, "bytes": nbytes, "workgroups": blocks,
+                    "us_per_launch": round(ms * 1e3, 3), "GB_s": round(gbs, 1),
+                    "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4), "rotation_bytes": nbytes * len(bufs)}
+            log(json.dumps(line))
+            lines.append(line)
+            if best is None or ms < best["us_per_launch"] / 1e3:
+                best = dict(line)
+        lines.append({"probe": "stream_read best", "launch": what, "bytes": nbytes,
+                      "us_per_launch": best["us_per_launch"], "GB_s": best["GB_s"],
+                      "frac_hbm_peak": best["frac_hbm_peak"], "workgroups": best["workgroups"]})
+        del bufs
+        torch.cuda.empty_cache()
+    return lines
+
+
+def _timed_cpu(fn, budget_s):
+    """Mean seconds per call of fn, repeated until budget_s has passed (at least twice, after one warm call)."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if n >= 2 and el >= budget_s:
+            return el / n
+
+
+def config_suite(reps: int, cpu: bool = True):
+    """Configurations 1, 2, 4 and 5 at their full sizes on the GPU, each with
+    the reference CPU path (the numpy restatement of _dequantize + float32
+    x @ W.T, or the float32 MoE) timed beside it on the host cores: warm
+    (float32 weights cached, the reference's steady state) and cold
+    (dequantization + matmul, its first use), plus one OpenBLAS thread for
+    the warm figure; configuration 1 also checks the GPU dequantization
+    bit-exact against the oracle's."""
+    import numpy as np
+    import torch
+
+    from dracort_amd.format.gguf import tensor_bytes
+    from dracort_amd.kernels import gguf_dequantize, gguf_gemm, gguf_gemv, gguf_moe, moe_workspace_bytes
+    from dracort_amd.runtime.decode import synthetic_weight
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    cores = len(os.sched_getaffinity(0))
+    out = {"cpu_cores": cores, "1": [], "2": [], "4": [], "5": []}
+    if cpu:
+        from threadpoolctl import threadpool_limits
+
+        from oracle import gguf_ref, matmul_ref
+
+    def cpu_gemv(t, n, k, blocks_dev, ms_list, xs, flops=False):
+        """{warm, cold, 1-thread} for the given activations xs (one per GPU line)."""
+        blocks = blocks_dev.cpu().numpy()
+        res = []
+        with threadpool_limits(limits=cores):
+            t0 = time.perf_counter()
+            w = gguf_ref.dequantize_matrix(t, blocks, (n, k))
+            t_dq = time.perf_counter() - t0
+            for x in xs:
+                t_mm = _timed_cpu(lambda: matmul_ref.cpu_linear_f32(x, w), 0.4)
+                res.append({"warm_s": t_mm, "cold_s": t_mm + t_dq})
+        with threadpool_limits(limits=1):
+            t1 = _timed_cpu(lambda: matmul_ref.cpu_linear_f32(xs[0], w), 0.4)
+        return w, res, t1
+
+    def gemv_gpu(t, n, k, m, xdtype):
+        nb = tensor_bytes(t, (n, k))
+        mats = rotation(lambda: synthetic_weight(n, k, t, gen, "cuda").data, nb, min_total=640 << 20)
+        x = torch.randn((m, k), device="cuda").to(xdtype)
+        y = torch.empty((m, n), device="cuda")
+        ms = time_launches([lambda w=w: gguf_gemv(x, w, t, (n, k), out=y) for w in mats], reps)
+        alg = nb + x.numel() * x.element_size() + y.numel() * 4
+        return mats, ms, alg
+
+    # 1: Q8_0 4096 x 4096, float32 x, M = 1; GPU dequant bit-exact vs the oracle's
+    mats, ms, alg = gemv_gpu(8, 4096, 4096, 1, torch.float32)
+    line = {"kernel": "decode GEMV", "ggml_type": "Q8_0", "shape": [4096, 4096], "m": 1, "x_dtype": "float32",
+            "us_per_launch": round(ms * 1e3, 3), "GB_s": round(alg / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "alg_bytes": alg}
+    if cpu:
+        xh = np.random.default_rng(1).standard_normal((1, 4096)).astype(np.float32)
+        w, res, t1 = cpu_gemv(8, 4096, 4096, mats[0], None, [xh])
+        gpu_w = gguf_dequantize(mats[0], 8, (4096, 4096)).cpu().numpy()
+        line["cpu"] = {"warm_GB_s": round(alg / res[0]["warm_s"] / 1e9, 2),
+                       "cold_GB_s": round(alg / res[0]["cold_s"] / 1e9, 3),
+                       "one_thread_warm_GB_s": round(alg / t1 / 1e9, 2), "cores": cores,
+                       "dequant_bit_exact": bool(np.array_equal(gpu_w.view(np.uint32), w.view(np.uint32)))}
+    out["1"].append(line)
+    del mats
+    # 2: Q4_0 at the four Llama-3-8B projection shapes, float32 x, M = 1 / 4 / 8
+    for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
+        lines = []
+        for m in (1, 4, 8):
+            mats, ms, alg = gemv_gpu(2, n, k, m, torch.float32)
+            lines.append({"kernel": "decode GEMV", "ggml_type": "Q4_0", "shape": [n, k], "m": m,
+                          "x_dtype": "float32", "us_per_launch": round(ms * 1e3, 3),
+                          "GB_s": round(alg / (ms * 1e-3) / 1e9, 1),
+                          "frac_hbm_peak": round(alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "alg_bytes": alg})
+            first = mats[0]
+            del mats
+        if cpu:
+            xs = [np.random.default_rng(m).standard_normal((m, k)).astype(np.float32) for m in (1, 4, 8)]
+            _, res, t1 = cpu_gemv(2, n, k, first, None, xs)
+            for ln, r in zip(lines, res):
+                ln["cpu"] = {"warm_GB_s": round(ln["alg_bytes"] / r["warm_s"] / 1e9, 2),
+                             "cold_GB_s": round(ln["alg_bytes"] / r["cold_s"] / 1e9, 3), "cores": cores}
+            lines[0]["cpu"]["one_thread_warm_GB_s"] = round(lines[0]["alg_bytes"] / t1 / 1e9, 2)
+        out["2"] += lines
+        torch.cuda.empty_cache()
+    # 4: prefill GEMM, Q4_K, bf16 x, M = 512 / 2048
+    for n, k in ((14336, 4096), (4096, 14336)):
+        wq = synthetic_weight(n, k, 12, gen, "cuda")
+        lines, xs = [], []
+        for m in (512, 2048):
+            x = torch.randn((m, k), device="cuda").to(torch.bfloat16)
+            y = torch.empty((m, n), device="cuda")
+            ms = time_launches([lambda: gguf_gemm(x, wq.data, 12, (n, k), out=y)], reps)
+            flops = 2.0 * m * n * k
+            lines.append({"kernel": "prefill GEMM", "ggml_type": "Q4_K", "shape": [n, k], "m": m,
+                          "us_per_launch": round(ms * 1e3, 2), "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1),
+                          "frac_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)})
+            xs.append(x.float().cpu().numpy())
+        if cpu:
+            blocks = wq.data.cpu().numpy()
+            with threadpool_limits(limits=cores):
+                t0 = time.perf_counter()
+                w = gguf_ref.dequantize_matrix(12, blocks, (n, k))
+                t_dq = time.perf_counter() - t0
+                for ln, x in zip(lines, xs):
+                    t_mm = _timed_cpu(lambda: matmul_ref.cpu_linear_f32(x, w), 0.5)
+                    fl = 2.0 * x.shape[0] * n * k
+                    ln["cpu"] = {"warm_GFLOP_s": round(fl / t_mm / 1e9, 1),
+                                 "cold_GFLOP_s": round(fl / (t_mm + t_dq) / 1e9, 1), "cores": cores}
+            with threadpool_limits(limits=1):
+                x0 = xs[0][:64]
+                t1 = _timed_cpu(lambda: matmul_ref.cpu_linear_f32(x0, w), 0.5)
+                lines[0]["cpu"]["one_thread_warm_GFLOP_s"] = round(2.0 * 64 * n * k / t1 / 1e9, 1)
+                lines[0]["cpu"]["one_thread_sample"] = "64 of the 512 rows"
+            del w
+        out["4"] += lines
+        del wq
+        torch.cuda.empty_cache()
+    # 5: Mixtral-8x7B-shaped MoE FFN, 8 Q4_K experts, 64 bf16 tokens, top-2
+    hid, inter, ne, tok = 4096, 14336, 8, 64
+    wg = [synthetic_weight(inter, hid, 12, gen, "cuda").data for _ in range(ne)]
+    wu = [synthetic_weight(inter, hid, 12, gen, "cuda").data for _ in range(ne)]
+    wd = [synthetic_weight(hid, inter, 12, gen, "cuda").data for _ in range(ne)]
+    x = torch.randn((tok, hid), device="cuda").to(torch.bfloat16)
+    logits = torch.randn((tok, ne), device="cuda")
+    ws = torch.empty(moe_workspace_bytes(tok, hid, inter, ne, 2), dtype=torch.uint8, device="cuda")
+    y = torch.empty((tok, hid), device="cuda")
+    ms = time_launches([lambda: gguf_moe(x, logits, wg, wu, wd, 12, inter, top_k=2, workspace=ws, out=y)], reps)
+    wbytes = sum(t.numel() for t in wg + wu + wd)
+    line = {"kernel": "MoE FFN (route + grouped expert GEMVs + combine)", "experts": ne, "tokens": tok, "top_k": 2,
+            "us_per_call": round(ms * 1e3, 2), "weight_bytes": wbytes, "GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    if cpu:
+        # a bounded sample: experts 0 and 1 with the tokens routed to them, scaled to the 8 experts
+        xh, lg = x.float().cpu().numpy(), logits.cpu().numpy()
+        idx, _ = matmul_ref.route_ref(lg, 2)
+        with threadpool_limits(limits=cores):
+            t0 = time.perf_counter()
+            exps = [(gguf_ref.dequantize_matrix(12, wg[e].cpu().numpy(), (inter, hid)),
+                     gguf_ref.dequantize_matrix(12, wu[e].cpu().numpy(), (inter, hid)),
+                     gguf_ref.dequantize_matrix(12, wd[e].cpu().numpy(), (hid, inter))) for e in range(2)]
+            t_dq = time.perf_counter() - t0
+            # the real routing; only experts 0 and 1 carry weights, so exactly their token sets are computed
+            t_mm = _timed_cpu(lambda: matmul_ref.cpu_moe_f32(xh, lg, exps, 2), 1.0)
+        share = (idx < 2).sum() / idx.size  # the sample's fraction of the 128 (token, expert) pairs
+        scale = 1.0 / max(share, 1e-9)
+        line["cpu"] = {"warm_GB_s": round(wbytes / (t_mm * scale) / 1e9, 2),
+                       "cold_GB_s": round(wbytes / ((t_mm + t_dq) * scale) / 1e9, 3), "cores": cores,
+                       "sample": f"experts 0-1 ({int((idx < 2).sum())} of 128 token-expert pairs), scaled to all 8"}
+        del exps
+    out["5"].append(line)
+    del wg, wu, wd
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -437,6 +658,10 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true", help="run only the roofline rotation + a 256 MB copy")
     ap.add_argument("--mfma-probe", action="store_true", help="run only the configuration-4 GEMMs (counter runs)")
     ap.add_argument("--moe-probe", action="store_true", help="run only the configuration-5 MoE FFN (kernel traces)")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="time a read-only kernel on each decode-launch size (the single-launch ceiling)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip configurations 1, 2, 4, 5 (GPU and CPU) in the default run")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -471,6 +696,10 @@ def main() -> int:
         return 0
     if args.moe_probe:
         moe_probe(3)
+        return 0
+    if args.stream_probe:
+        for line in stream_probe(args.roofline_reps):
+            print(json.dumps(line), flush=True)
         return 0
     shape = LlamaShape()
     t0 = time.time()
@@ -513,6 +742,12 @@ def main() -> int:
     dom = step_dominant_roofline(ls, args.roofline_reps)
     log(f"step-dominant launch: {dom}")
 
+    configs = None
+    if not args.no_configs:
+        t0 = time.time()
+        configs = config_suite(max(5, args.roofline_reps // 2), cpu=not args.no_cpu_baseline)
+        log(f"configurations 1, 2, 4, 5 ({time.time() - t0:.1f} s): {json.dumps(configs)}")
+
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.time()
@@ -551,6 +786,7 @@ def main() -> int:
         "roofline": roof,
         "roofline_step_dominant": dom,
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
     return 0

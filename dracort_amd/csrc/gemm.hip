@@ -20,8 +20,13 @@
 // zero at K = 4096 with outlier rows.  The activations are bf16 and exact.
 // The next K step's global loads are issued before the MFMAs of the current
 // one so that HBM latency overlaps the matrix work.
+//
+// Q4_K with a workspace takes the exact f16 kernels instead: gemm_q4k2.h
+// (256 x 128 tiles of 32 x 32 x 16 MFMAs) when its grid fills at least three
+// quarters of the CUs, gemm_q4k.h (128 x 128 tiles) for smaller problems.
 #include "draco_internal.h"
 #include "gemm_q4k.h"
+#include "gemm_q4k2.h"
 #include "gemv_core.h"
 
 namespace draco {
@@ -219,7 +224,8 @@ int gemm_dispatch(int qtype, bool d_last, const void* w, const void* x, const fl
   if (qtype == kQ4_K && workspace) {
     if ((int64_t)n * (k / 256) * 144 >= ((int64_t)1 << 31))
       return set_error(DRACO_EINVAL_SHAPE, "Q4_K GEMM weight above 2 GiB");
-    return launch_gemm_q4k(w, x, bias, y, m, n, k, workspace, s);
+    return gemm_q4k2_fits(m, n) ? launch_gemm_q4k2(w, x, bias, y, m, n, k, workspace, s)
+                                : launch_gemm_q4k(w, x, bias, y, m, n, k, workspace, s);
   }
   switch (qtype) {
     case kQ8_0: return launch_gemm<kQ8_0, false>(w, x, bias, y, m, n, k, s);

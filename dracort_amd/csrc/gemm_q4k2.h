@@ -1,0 +1,316 @@
+// Prefill GEMM for Q4_K weights on the 32 x 32 x 16 f16 matrix cores (gfx950).
+//
+// The same arithmetic as gemm_q4k.h (every product exact: B = sc q in f16,
+// <= 945; the activations f16 after the per-row power-of-two normalisation of
+// gemm_prep_kernel; per super-block one MFMA chain D1 = sum x sc q scaled once
+// by d, and the min term D2 = sum_j m_j S_j from bf16 MFMAs over the three
+// bf16 planes of the 32-element sums S, scaled once by dmin), on larger
+// tiles:
+//   * v_mfma_f32_32x32x16_f16: 32 x 32 outputs per instruction, twice the
+//     FLOP per LDS fragment byte of 16 x 16 x 32, and its full rate with one
+//     wave per SIMD (measured 2.07 PFLOP/s in a pure-MFMA loop, where the
+//     16 x 16 x 32 form needs two waves to pass 1.25);
+//   * each wave owns a 64 x 64 output tile (2 x 2 MFMA tiles: two A and two B
+//     fragment reads feed four MFMAs per 16-deep slice);
+//   * a workgroup of WM x WN waves owns a (64 WM tokens) x (64 WN weight rows)
+//     tile, so each converted weight code feeds 64 WM tokens.
+// Per K step of 64 (half a super-block's sub-block pairs: sub-blocks 2p and
+// 2p + 1 of super-block sb at step 4 sb + p) the workgroup stages the f16
+// activation tile and the converted f16 sc q tile in LDS, double-buffered
+// with the global loads two steps ahead; at a super-block's first step it
+// also stages the sums, the mins and d / dmin.  The output is y = acc * 2^t
+// (the row's prep scale) + bias.
+#pragma once
+
+#include "draco_internal.h"
+#include "gemm_q4k.h"
+#include "gemv_core.h"
+#include "gemv_stream.h"
+
+namespace draco {
+
+typedef _Float16 g2_f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 g2_f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 g2_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float g2_f32x16 __attribute__((ext_vector_type(16)));
+typedef int g2_v4i __attribute__((ext_vector_type(4)));
+typedef int g2_v2i __attribute__((ext_vector_type(2)));
+
+template <int WM, int WN, int NS = 2>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* __restrict__ w, GemmQ4kWs ws,
+                                                                 const float* __restrict__ bias,
+                                                                 float* __restrict__ y, int M, int N, int K,
+                                                                 int tiles_m) {
+  constexpr int NT = WM * WN * 64;          // threads
+  constexpr int BM = 64 * WM, BN = 64 * WN;  // workgroup tile
+  constexpr int BK = 64, LDK = BK + 8;       // f16 per LDS row (144 B)
+  constexpr int APT = BM * BK / 8 / NT;      // 16-byte activation pieces per thread per step
+  constexpr int BPT = BN * 4 / NT;           // 8-byte code pieces per thread per step (1 or 2)
+  constexpr int SPT = (3 * BM + NT - 1) / NT;  // 16-byte sum pieces per thread per super-block
+  static_assert(APT >= 1 && BPT >= 1, "tile too small for the workgroup");
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LDK];
+  __shared__ uint4 Ss[2][3][BM];  // [super-block parity][plane][token]: 8 sub-block sums (bf16)
+  __shared__ uint4 Ms[2][BN];     // [parity][weight row]: 8 mins (bf16)
+  __shared__ float2 Ds[2][BN];    // [parity][weight row]: d, dmin
+  __shared__ uint2 Sc[2][BN];     // [parity][weight row]: the eight 6-bit sub-block scales
+
+  // XCD-aware order: workgroups are dealt to the 8 XCDs round robin; renumber
+  // so each XCD gets a contiguous run of tiles (the token tiles of one weight
+  // tile share that XCD's L2)
+  const int nb = gridDim.x;
+  int bid = blockIdx.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  const int tm = bid % tiles_m, tn = bid / tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % WM, wn = wave / WM;
+  const int sbs = K >> 8, groups = K >> 5, steps = K / BK;
+  const uint32_t row_bytes = (uint32_t)sbs * 144u;
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(w, (uint32_t)N * row_bytes);
+
+  // global data of one step, in a ring of NS register sets (step s in set s % NS)
+  static_assert(NS == 2 || NS == 4, "the ring index must be static in the 4-step super-block loop");
+  struct Set {
+    uint4 a[APT];
+    uint2 b[BPT];
+    uint4 h;
+    uint4 s[SPT];
+  } set[NS];
+  auto load = [&](Set& st, int ks) {
+    const int k0 = ks * BK, sb = ks >> 2, p = ks & 3;
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+      const int idx = tid + NT * i;
+      const int row = idx >> 3, c8 = idx & 7;
+      st.a[i] = m0 + row < M ? *reinterpret_cast<const uint4*>(ws.xh + (size_t)(m0 + row) * K + k0 + 8 * c8)
+                             : uint4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      const int idx = tid + NT * i;
+      const int br = idx >> 2, bq = idx & 3;
+      const int wrow = (int)((uint32_t)min(n0 + br, N - 1) * row_bytes);
+      const g2_v2i q = __builtin_amdgcn_raw_buffer_load_b64(wrs, wrow + sb * 144 + 16 + 32 * p + 8 * bq, 0, 0);
+      st.b[i] = uint2{(uint32_t)q.x, (uint32_t)q.y};
+    }
+    if (p == 0) {
+      if (tid < BN) {
+        const int wrow = (int)((uint32_t)min(n0 + tid, N - 1) * row_bytes);
+        const g2_v4i hd = __builtin_amdgcn_raw_buffer_load_b128(wrs, wrow + sb * 144, 0, 0);
+        st.h = uint4{(uint32_t)hd.x, (uint32_t)hd.y, (uint32_t)hd.z, (uint32_t)hd.w};
+      }
+#pragma unroll
+      for (int i = 0; i < SPT; ++i) {
+        const int idx = tid + NT * i;
+        const int pl = idx / BM, row = idx - pl * BM;
+        st.s[i] = (idx < 3 * BM && m0 + row < M)
+                      ? *reinterpret_cast<const uint4*>(ws.sp + (size_t)pl * M * groups + (size_t)(m0 + row) * groups +
+                                                        8 * sb)
+                      : uint4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+
+  // LDS image of step ks (buffer ks & 1) from a register set
+  auto stage = [&](const Set& st, int ks) {
+    const int buf = ks & 1, sb = ks >> 2, p = ks & 3, par = sb & 1;
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+      const int idx = tid + NT * i;
+      *reinterpret_cast<uint4*>(&As[buf][(idx >> 3) * LDK + 8 * (idx & 7)]) = st.a[i];
+    }
+    if (p == 0) {
+      if (tid < BN) {
+        const uint32_t s0 = st.h.y, s1 = st.h.z, s2 = st.h.w;
+        const uint32_t sc_lo = s0 & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+        const uint32_t m_lo = s1 & 0x3F3F3F3Fu;
+        const uint32_t m_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+        uint32_t mb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t mw = j < 2 ? m_lo : m_hi;
+          const int sh = 16 * (j & 1);
+          mb[j] = gq_bf16_rne((float)((mw >> sh) & 0xFFu)) | (gq_bf16_rne((float)((mw >> (sh + 8)) & 0xFFu)) << 16);
+        }
+        Ms[par][tid] = uint4{mb[0], mb[1], mb[2], mb[3]};
+        Ds[par][tid] = float2{f16_bits_to_f32(st.h.x), f16_bits_to_f32(st.h.x >> 16)};
+        Sc[par][tid] = uint2{sc_lo, sc_hi};
+      }
+#pragma unroll
+      for (int i = 0; i < SPT; ++i) {
+        const int idx = tid + NT * i;
+        if (idx < 3 * BM) Ss[par][idx / BM][idx % BM] = st.s[i];
+      }
+    }
+  };
+  // codes of sub-blocks 2p (low nibbles) and 2p + 1 (high nibbles) times their
+  // scales, as f16, into the LDS B image (after the step's scales are staged)
+  auto stage_codes = [&](const Set& st, int ks) {
+    const int buf = ks & 1, sb = ks >> 2, p = ks & 3, par = sb & 1;
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      const int idx = tid + NT * i;
+      const int br = idx >> 2, bq = idx & 3;
+      const uint2 scw2 = Sc[par][br];
+      const uint32_t scw = p < 2 ? scw2.x : scw2.y;
+      const int sh = 16 * (p & 1);
+      const _Float16 s_a = (_Float16)(float)((scw >> sh) & 0xFFu), s_b = (_Float16)(float)((scw >> (sh + 8)) & 0xFFu);
+      const g2_f16x2 sa2 = {s_a, s_a}, sb2 = {s_b, s_b};
+      const g2_f16x2 ca2 = {(_Float16)(-1024.f) * s_a, (_Float16)(-1024.f) * s_a};
+      const g2_f16x2 cb2 = {(_Float16)(-1024.f) * s_b, (_Float16)(-1024.f) * s_b};
+      const uint32_t qw[2] = {st.b[i].x, st.b[i].y};
+      uint32_t lo[4], hi[4];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t cl = qw[e] & 0x0F0F0F0Fu, chh = (qw[e] >> 4) & 0x0F0F0F0Fu;
+        // f16 bits 0x64qq = 1024 + q; fma(1024 + q, s, -1024 s) = s q exactly
+        lo[2 * e] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
+            __builtin_bit_cast(g2_f16x2, __builtin_amdgcn_perm(0x64646464u, cl, 0x04010400u)), sa2, ca2));
+        lo[2 * e + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
+            __builtin_bit_cast(g2_f16x2, __builtin_amdgcn_perm(0x64646464u, cl, 0x04030402u)), sa2, ca2));
+        hi[2 * e] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
+            __builtin_bit_cast(g2_f16x2, __builtin_amdgcn_perm(0x64646464u, chh, 0x04010400u)), sb2, cb2));
+        hi[2 * e + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(
+            __builtin_bit_cast(g2_f16x2, __builtin_amdgcn_perm(0x64646464u, chh, 0x04030402u)), sb2, cb2));
+      }
+      uint16_t* brow = &Bs[buf][br * LDK];
+      *reinterpret_cast<uint4*>(brow + 8 * bq) = uint4{lo[0], lo[1], lo[2], lo[3]};
+      *reinterpret_cast<uint4*>(brow + 32 + 8 * bq) = uint4{hi[0], hi[1], hi[2], hi[3]};
+    }
+  };
+
+  g2_f32x16 acc[2][2], d1[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        acc[i][j][v] = 0.f;
+        d1[i][j][v] = 0.f;
+      }
+  // fragment lane roles: row / column l % 32, k slice 8 (l / 32)
+  const int fr = lane & 31, fk = 8 * (lane >> 5);
+  const uint4 z = {0u, 0u, 0u, 0u};
+
+#pragma unroll
+  for (int i = 0; i < NS; ++i)
+    if (i < steps) load(set[i], i);
+  stage(set[0], 0);
+  __syncthreads();
+  stage_codes(set[0], 0);
+  if (NS < steps) load(set[0], NS);
+  __syncthreads();
+  for (int sb = 0; sb < sbs; ++sb) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int ks = 4 * sb + p;
+      const int buf = p & 1;
+      // stage the next step into the other buffer, then refill its register set
+      if (ks + 1 < steps) {
+        Set& nx = set[(p + 1) % NS];
+        stage(nx, ks + 1);
+        if (((ks + 1) & 3) == 0) __syncthreads();  // the new super-block's scales before the codes
+        stage_codes(nx, ks + 1);
+        if (ks + 1 + NS < steps) load(nx, ks + 1 + NS);
+      }
+      // multiply step ks: four 16-deep slices, 2 x 2 MFMA tiles
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        g2_f16x8 a[2], b[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          a[i] = *reinterpret_cast<const g2_f16x8*>(&As[buf][(wm * 64 + 32 * i + fr) * LDK + 16 * kk + fk]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          b[j] = *reinterpret_cast<const g2_f16x8*>(&Bs[buf][(wn * 64 + 32 * j + fr) * LDK + 16 * kk + fk]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) d1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], d1[i][j], 0, 0, 0);
+      }
+      if (p == 3) {
+        // super-block end: min term on the bf16 matrix cores (k positions
+        // 0..7 of the 16 carry the eight sub-block sums / mins), then
+        // acc += d D1 - dmin D2
+        const int par = sb & 1;
+        g2_bf16x8 bm[2];
+        float dd[2], dm[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int col = wn * 64 + 32 * j + fr;
+          bm[j] = __builtin_bit_cast(g2_bf16x8, lane < 32 ? Ms[par][col] : z);
+          const float2 dv = Ds[par][col];
+          dd[j] = dv.x;
+          dm[j] = dv.y;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          g2_bf16x8 sa[3];
+#pragma unroll
+          for (int pl = 0; pl < 3; ++pl)
+            sa[pl] = __builtin_bit_cast(g2_bf16x8, lane < 32 ? Ss[par][pl][wm * 64 + 32 * i + fr] : z);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            g2_f32x16 d2;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) d2[v] = 0.f;
+            d2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sa[2], bm[j], d2, 0, 0, 0);
+            d2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sa[1], bm[j], d2, 0, 0, 0);
+            d2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sa[0], bm[j], d2, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              acc[i][j][v] = fmaf(dd[j], d1[i][j][v], acc[i][j][v]);
+              acc[i][j][v] = fmaf(-dm[j], d2[v], acc[i][j][v]);
+              d1[i][j][v] = 0.f;
+            }
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // D layout: lane l, register v holds row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = m0 + wm * 64 + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+      if (m >= M) continue;
+      const float rs = ws.rsc[m];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + 32 * j + fr;
+        if (n < N) y[(size_t)m * N + n] = acc[i][j][v] * rs + (bias ? bias[n] : 0.f);
+      }
+    }
+}
+
+// Whether the 256 x 128 tiling fills the GPU for this shape (enough
+// workgroups for three quarters of the CUs); otherwise gemm_q4k.h's 64-token
+// tiles give more parallelism (measured on MI355X: 14336 x 4096 at M = 512
+// 122 us here vs 176 us; 4096 x 14336 at M = 512, 64 workgroups, 336 us here
+// vs 209 us there).
+inline bool gemm_q4k2_fits(int m, int n) {
+  return (int64_t)((m + 255) / 256) * ((n + 127) / 128) * 4 >= (int64_t)device_cus() * 3;
+}
+
+// Launches the activation prep and the GEMM; `workspace` holds
+// gemm_q4k_ws_layout(m, k) bytes.
+inline int launch_gemm_q4k2(const void* w, const void* x, const float* bias, float* y, int m, int n, int k,
+                            void* workspace, hipStream_t s) {
+  GemmQ4kWs ws;
+  gemm_q4k_ws_layout(m, k, static_cast<char*>(workspace), &ws);
+  hipLaunchKernelGGL(gemm_prep_kernel, dim3((unsigned)m), dim3(256), 0, s, static_cast<const uint16_t*>(x), m, k, ws);
+  if (int rc = check_launch("gemm_prep")) return rc;
+  const int tiles_n = (n + 127) / 128, tiles_m = (m + 255) / 256;
+  hipLaunchKernelGGL((gemm_q4k2_kernel<4, 2>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, s,
+                     static_cast<const uint8_t*>(w), ws, bias, y, m, n, k, tiles_m);
+  return check_launch("gemm_q4k2");
+}
+
+}  // namespace draco

@@ -440,8 +440,8 @@ def stream_probe(reps: int):
 
     lib = ctypes.CDLL(PROBE_LIB)
     lib.draco_probe_stream_read.restype = ctypes.c_int
-    lib.draco_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
-                                            ctypes.c_void_p]
+    lib.draco_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_void_p, ctypes.c_void_p]
     sink = torch.zeros(256, dtype=torch.int32, device="cuda")
     sizes = {"o 4096x4096 Q4_K": 9437184, "q/k/v 6144x4096 Q4_K": 14155776, "gate 14336x4096 Q4_K": 33030144,
              "down 4096x14336 Q6_K": 48168960, "gate+up 2x14336x4096 Q4_K": 66060288}
@@ -451,25 +451,27 @@ def stream_probe(reps: int):
         bufs = rotation(lambda: torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_(0, 255), nbytes)
         best = None
         for per_cu in (1, 2, 4, 8):
-            blocks = cus * per_cu
+            for loads in (4, 8, 16):
+                blocks = cus * per_cu
 
-            def launch(b=None, blocks=blocks):
-                rc = lib.draco_probe_stream_read(b.data_ptr(), nbytes, blocks, sink.data_ptr(),
-                                                 torch.cuda.current_stream().cuda_stream)
-                assert rc == 0, rc
+                def launch(b=None, blocks=blocks, loads=loads):
+                    rc = lib.draco_probe_stream_read(b.data_ptr(), nbytes, blocks, loads, sink.data_ptr(),
+                                                     torch.cuda.current_stream().cuda_stream)
+                    assert rc == 0, rc
 
-            ms = time_launches([lambda b=b: launch(b) for b in bufs], reps)
-            gbs = nbytes / (ms * 1e-3) / 1e9
-            line = {"probe": "stream_read", "launch": what, "bytes": nbytes, "workgroups": blocks,
-                    "us_per_launch": round(ms * 1e3, 3), "GB_s": round(gbs, 1),
-                    "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4), "rotation_bytes": nbytes * len(bufs)}
-            log(json.dumps(line))
-            lines.append(line)
-            if best is None or ms < best["us_per_launch"] / 1e3:
-                best = dict(line)
+                ms = time_launches([lambda b=b: launch(b) for b in bufs], reps)
+                gbs = nbytes / (ms * 1e-3) / 1e9
+                line = {"probe": "stream_read", "launch": what, "bytes": nbytes, "workgroups": blocks,
+                        "loads_in_flight": loads, "us_per_launch": round(ms * 1e3, 3), "GB_s": round(gbs, 1),
+                        "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4), "rotation_bytes": nbytes * len(bufs)}
+                log(json.dumps(line))
+                lines.append(line)
+                if best is None or ms < best["us_per_launch"] / 1e3:
+                    best = dict(line)
         lines.append({"probe": "stream_read best", "launch": what, "bytes": nbytes,
                       "us_per_launch": best["us_per_launch"], "GB_s": best["GB_s"],
-                      "frac_hbm_peak": best["frac_hbm_peak"], "workgroups": best["workgroups"]})
+                      "frac_hbm_peak": best["frac_hbm_peak"], "workgroups": best["workgroups"],
+                      "loads_in_flight": best["loads_in_flight"]})
         del bufs
         torch.cuda.empty_cache()
     return lines

@@ -367,13 +367,13 @@ int draco_gguf_gemm(int ggml_type, const void* w, size_t w_bytes, const void* x_
   if (int rc = check_ptr(x_bf16, "x")) return rc;
   if (int rc = check_ptr(y, "y")) return rc;
   if (workspace) {
-    const size_t need = gemm_workspace_size(t.base, m, k);
+    const size_t need = gemm_workspace_min(t.base, m, k);
     if (workspace_bytes < need)
       return set_error(DRACO_EWORKSPACE, "GEMM workspace needs %zu bytes, got %zu", need, workspace_bytes);
     if (reinterpret_cast<uintptr_t>(workspace) & 255u)
       return set_error(DRACO_EINVAL_ARG, "GEMM workspace must be 256-byte aligned");
   }
-  return gemm_dispatch(t.base, t.d_last, w, x_bf16, bias, y, (int)m, (int)n, (int)k, workspace,
+  return gemm_dispatch(t.base, t.d_last, w, x_bf16, bias, y, (int)m, (int)n, (int)k, workspace, workspace_bytes,
                        static_cast<hipStream_t>(stream));
 }
 
@@ -407,7 +407,7 @@ int draco_gguf_linear_noalloc(int ggml_type, const void* w, size_t w_bytes, cons
   if (int rc = decode_type(ggml_type, &t)) return rc;
   if (m < 1 || m > kMaxDim || k < 1 || k > kMaxDim)
     return set_error(DRACO_EINVAL_SHAPE, "invalid token count %lld or row length %lld", (long long)m, (long long)k);
-  const size_t need = gemm_workspace_size(t.base, m, k);
+  const size_t need = gemm_workspace_min(t.base, m, k);
   if (need == 0)  // this type's GEMM needs no workspace
     return draco_gguf_gemm(ggml_type, w, w_bytes, x, bias, y, m, n, k, nullptr, 0, stream);
   if (need > (size_t)DRACO_GGUF_NOALLOC_SCRATCH_BYTES)

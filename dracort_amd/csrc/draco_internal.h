@@ -53,11 +53,15 @@ int gemv_swiglu_norm_dispatch(int qtype, bool d_last, const void* w_gate, const 
                               const float* x, const float* norm_w, float eps, uint16_t* x_norm, int m, int n, int k,
                               hipStream_t s);
 
-// Workspace bytes of the GEMM of this base type (0: it needs none).
+// Workspace bytes of the GEMM of this base type (0: it needs none): the
+// minimum its workspace kernels require, and the size that also holds the
+// split-K partial sums of the few-tile shapes.
+size_t gemm_workspace_min(int qtype, int64_t m, int64_t k);
 size_t gemm_workspace_size(int qtype, int64_t m, int64_t k);
 
-// workspace: NULL, or gemm_workspace_size(qtype, m, k) bytes, 256-byte aligned.
+// workspace: NULL, or at least gemm_workspace_min(qtype, m, k) bytes (256-byte
+// aligned), of which workspace_bytes are usable.
 int gemm_dispatch(int qtype, bool d_last, const void* w, const void* x_bf16, const float* bias, float* y,
-                  int m, int n, int k, void* workspace, hipStream_t s);
+                  int m, int n, int k, void* workspace, size_t workspace_bytes, hipStream_t s);
 
 }  // namespace draco

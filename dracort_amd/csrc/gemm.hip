@@ -22,8 +22,10 @@
 // one so that HBM latency overlaps the matrix work.
 //
 // Q4_K with a workspace takes the exact f16 kernels instead: gemm_q4k2.h
-// (256 x 128 tiles of 32 x 32 x 16 MFMAs) when its grid fills at least three
-// quarters of the CUs, gemm_q4k.h (128 x 128 tiles) for smaller problems.
+// (256 x 128 tiles of 32 x 32 x 16 MFMAs, split along K when there are too
+// few tiles and the workspace has room for the partial sums) when its grid
+// fills at least three quarters of the CUs, gemm_q4k.h (64 x 128 tiles)
+// otherwise.
 #include "draco_internal.h"
 #include "gemm_q4k.h"
 #include "gemm_q4k2.h"
@@ -215,17 +217,23 @@ static int launch_gemm(const void* w, const void* x, const float* bias, float* y
   return check_launch("gemm");
 }
 
-size_t gemm_workspace_size(int qtype, int64_t m, int64_t k) {
+size_t gemm_workspace_min(int qtype, int64_t m, int64_t k) {
   return qtype == kQ4_K ? gemm_q4k_ws_layout(m, k, nullptr, nullptr) : 0;
 }
 
+size_t gemm_workspace_size(int qtype, int64_t m, int64_t k) {
+  return qtype == kQ4_K ? gemm_q4k_ws_layout(m, k, nullptr, nullptr) + gemm_q4k2_part_bound(m) : 0;
+}
+
 int gemm_dispatch(int qtype, bool d_last, const void* w, const void* x, const float* bias, float* y, int m, int n,
-                  int k, void* workspace, hipStream_t s) {
+                  int k, void* workspace, size_t workspace_bytes, hipStream_t s) {
   if (qtype == kQ4_K && workspace) {
     if ((int64_t)n * (k / 256) * 144 >= ((int64_t)1 << 31))
       return set_error(DRACO_EINVAL_SHAPE, "Q4_K GEMM weight above 2 GiB");
-    return gemm_q4k2_fits(m, n) ? launch_gemm_q4k2(w, x, bias, y, m, n, k, workspace, s)
-                                : launch_gemm_q4k(w, x, bias, y, m, n, k, workspace, s);
+    const size_t base = gemm_q4k_ws_layout(m, k, nullptr, nullptr);
+    const GemmQ4k2Plan plan = gemm_q4k2_plan(m, n, k, workspace_bytes > base ? workspace_bytes - base : 0);
+    return plan.splits ? launch_gemm_q4k2(w, x, bias, y, m, n, k, workspace, plan, s)
+                       : launch_gemm_q4k(w, x, bias, y, m, n, k, workspace, s);
   }
   switch (qtype) {
     case kQ8_0: return launch_gemm<kQ8_0, false>(w, x, bias, y, m, n, k, s);

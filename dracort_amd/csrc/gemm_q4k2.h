@@ -22,6 +22,8 @@
 // (the row's prep scale) + bias.
 #pragma once
 
+#include <algorithm>
+
 #include "draco_internal.h"
 #include "gemm_q4k.h"
 #include "gemv_core.h"
@@ -36,11 +38,23 @@ typedef float g2_f32x16 __attribute__((ext_vector_type(16)));
 typedef int g2_v4i __attribute__((ext_vector_type(4)));
 typedef int g2_v2i __attribute__((ext_vector_type(2)));
 
+// tid again, as a value the compiler cannot prove equal to tid: offsets used
+// once per super-block are recomputed there instead of held in registers
+// across the loop (the register budget is spent on the tiles)
+__device__ __forceinline__ int g2_fresh(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Split K: with part != nullptr the grid holds `splits` workgroups per output
+// tile, split s taking super-blocks [s sbps, (s + 1) sbps) and storing its raw
+// sums to part[s][M][N]; gemm_split_reduce_kernel adds them in split order.
 template <int WM, int WN, int NS = 2>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* __restrict__ w, GemmQ4kWs ws,
                                                                  const float* __restrict__ bias,
                                                                  float* __restrict__ y, int M, int N, int K,
-                                                                 int tiles_m) {
+                                                                 int tiles_m, int tiles, int sbps,
+                                                                 float* __restrict__ part) {
   constexpr int NT = WM * WN * 64;          // threads
   constexpr int BM = 64 * WM, BN = 64 * WN;  // workgroup tile
   constexpr int BK = 64, LDK = BK + 8;       // f16 per LDS row (144 B)
@@ -61,31 +75,49 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* 
   const int nb = gridDim.x;
   int bid = blockIdx.x;
   if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  const int split = bid / tiles;
+  bid -= split * tiles;
   const int tm = bid % tiles_m, tn = bid / tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WM, wn = wave / WM;
-  const int sbs = K >> 8, groups = K >> 5, steps = K / BK;
+  const int sbs = K >> 8, groups = K >> 5;
+  const int sb0 = split * sbps, sb1 = min(sb0 + sbps, sbs), ks0 = 4 * sb0;
   const uint32_t row_bytes = (uint32_t)sbs * 144u;
   const __amdgpu_buffer_rsrc_t wrs = make_rsrc(w, (uint32_t)N * row_bytes);
+  // activations and sums through buffer resources: 32-bit offsets, and reads
+  // past the end (token rows beyond M) return zero
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(ws.xh, (uint32_t)M * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(ws.sp, 3u * (uint32_t)M * (uint32_t)groups * 2u);
 
   // global data of one step, in a ring of NS register sets (step s in set s % NS)
   static_assert(NS == 2 || NS == 4, "the ring index must be static in the 4-step super-block loop");
   struct Set {
     uint4 a[APT];
     uint2 b[BPT];
+  } set[NS];
+  // a super-block's header and sums: one copy (loaded with the super-block's
+  // first step, at most NS - 1 steps ahead of its staging, which comes first
+  // in every iteration)
+  struct SbSet {
     uint4 h;
     uint4 s[SPT];
-  } set[NS];
+  } sbset;
+  // Every thread issues the same loads at every step, also past the last
+  // step and for rows / threads with nothing to fetch: offsets past a
+  // buffer's end read zero, and those within it (the next row, a later step)
+  // only feed LDS images that are never multiplied.  A fixed load count per
+  // step lets each wait leave the newer steps' loads in flight.
   auto load = [&](Set& st, int ks) {
     const int k0 = ks * BK, sb = ks >> 2, p = ks & 3;
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
       const int idx = tid + NT * i;
       const int row = idx >> 3, c8 = idx & 7;
-      st.a[i] = m0 + row < M ? *reinterpret_cast<const uint4*>(ws.xh + (size_t)(m0 + row) * K + k0 + 8 * c8)
-                             : uint4{0u, 0u, 0u, 0u};
+      const g2_v4i v = __builtin_amdgcn_raw_buffer_load_b128(
+          xrs, (uint32_t)(m0 + row) * (uint32_t)K * 2u + (uint32_t)(k0 + 8 * c8) * 2u, 0, 0);
+      st.a[i] = uint4{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
     }
 #pragma unroll
     for (int i = 0; i < BPT; ++i) {
@@ -96,19 +128,23 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* 
       st.b[i] = uint2{(uint32_t)q.x, (uint32_t)q.y};
     }
     if (p == 0) {
-      if (tid < BN) {
-        const int wrow = (int)((uint32_t)min(n0 + tid, N - 1) * row_bytes);
-        const g2_v4i hd = __builtin_amdgcn_raw_buffer_load_b128(wrs, wrow + sb * 144, 0, 0);
-        st.h = uint4{(uint32_t)hd.x, (uint32_t)hd.y, (uint32_t)hd.z, (uint32_t)hd.w};
+      const int tid = g2_fresh(threadIdx.x);
+      {
+        const uint32_t off = tid < BN ? (uint32_t)min(n0 + tid, N - 1) * row_bytes + (uint32_t)sb * 144u : 0xFFFFFFF0u;
+        const g2_v4i hd = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
+        sbset.h = uint4{(uint32_t)hd.x, (uint32_t)hd.y, (uint32_t)hd.z, (uint32_t)hd.w};
       }
 #pragma unroll
       for (int i = 0; i < SPT; ++i) {
         const int idx = tid + NT * i;
         const int pl = idx / BM, row = idx - pl * BM;
-        st.s[i] = (idx < 3 * BM && m0 + row < M)
-                      ? *reinterpret_cast<const uint4*>(ws.sp + (size_t)pl * M * groups + (size_t)(m0 + row) * groups +
-                                                        8 * sb)
-                      : uint4{0u, 0u, 0u, 0u};
+        // rows past M read a neighbouring plane or past the end: they feed
+        // only output rows that are never stored
+        const uint32_t off = idx < 3 * BM ? ((uint32_t)pl * (uint32_t)M + (uint32_t)(m0 + row)) * (uint32_t)groups * 2u +
+                                                (uint32_t)sb * 16u
+                                          : 0xFFFFFFF0u;
+        const g2_v4i v = __builtin_amdgcn_raw_buffer_load_b128(srs, off, 0, 0);
+        sbset.s[i] = uint4{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
       }
     }
   };
@@ -122,8 +158,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* 
       *reinterpret_cast<uint4*>(&As[buf][(idx >> 3) * LDK + 8 * (idx & 7)]) = st.a[i];
     }
     if (p == 0) {
+      const int tid = g2_fresh(threadIdx.x);
       if (tid < BN) {
-        const uint32_t s0 = st.h.y, s1 = st.h.z, s2 = st.h.w;
+        const uint32_t s0 = sbset.h.y, s1 = sbset.h.z, s2 = sbset.h.w;
         const uint32_t sc_lo = s0 & 0x3F3F3F3Fu;
         const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
         const uint32_t m_lo = s1 & 0x3F3F3F3Fu;
@@ -136,13 +173,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* 
           mb[j] = gq_bf16_rne((float)((mw >> sh) & 0xFFu)) | (gq_bf16_rne((float)((mw >> (sh + 8)) & 0xFFu)) << 16);
         }
         Ms[par][tid] = uint4{mb[0], mb[1], mb[2], mb[3]};
-        Ds[par][tid] = float2{f16_bits_to_f32(st.h.x), f16_bits_to_f32(st.h.x >> 16)};
+        Ds[par][tid] = float2{f16_bits_to_f32(sbset.h.x), f16_bits_to_f32(sbset.h.x >> 16)};
         Sc[par][tid] = uint2{sc_lo, sc_hi};
       }
 #pragma unroll
       for (int i = 0; i < SPT; ++i) {
         const int idx = tid + NT * i;
-        if (idx < 3 * BM) Ss[par][idx / BM][idx % BM] = st.s[i];
+        if (idx < 3 * BM) Ss[par][idx / BM][idx % BM] = sbset.s[i];
       }
     }
   };
@@ -182,44 +219,44 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* 
     }
   };
 
+  g2_f32x16 zero16;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) zero16[v] = 0.f;
   g2_f32x16 acc[2][2], d1[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        acc[i][j][v] = 0.f;
-        d1[i][j][v] = 0.f;
-      }
+    for (int j = 0; j < 2; ++j) acc[i][j] = zero16;
   // fragment lane roles: row / column l % 32, k slice 8 (l / 32)
   const int fr = lane & 31, fk = 8 * (lane >> 5);
   const uint4 z = {0u, 0u, 0u, 0u};
 
 #pragma unroll
-  for (int i = 0; i < NS; ++i)
-    if (i < steps) load(set[i], i);
-  stage(set[0], 0);
+  for (int i = 0; i < NS; ++i) load(set[i], ks0 + i);
+  stage(set[0], ks0);
   __syncthreads();
-  stage_codes(set[0], 0);
-  if (NS < steps) load(set[0], NS);
+  stage_codes(set[0], ks0);
+  load(set[0], ks0 + NS);
   __syncthreads();
-  for (int sb = 0; sb < sbs; ++sb) {
+  for (int sb = sb0; sb < sb1; ++sb) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const int ks = 4 * sb + p;
       const int buf = p & 1;
-      // stage the next step into the other buffer, then refill its register set
-      if (ks + 1 < steps) {
+      // stage the next step into the other buffer, then refill its register
+      // set (after the last step this stages an image nobody reads)
+      auto stage_next = [&]() {
         Set& nx = set[(p + 1) % NS];
         stage(nx, ks + 1);
         if (((ks + 1) & 3) == 0) __syncthreads();  // the new super-block's scales before the codes
         stage_codes(nx, ks + 1);
-        if (ks + 1 + NS < steps) load(nx, ks + 1 + NS);
-      }
-      // multiply step ks: four 16-deep slices, 2 x 2 MFMA tiles
+        load(nx, ks + 1 + NS);
+      };
+      // multiply step ks: four 16-deep slices, 2 x 2 MFMA tiles; the next
+      // step is staged after the third, while the matrix cores still work
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
+        if (kk == 3) stage_next();
         g2_f16x8 a[2], b[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -230,7 +267,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* 
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j) d1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], d1[i][j], 0, 0, 0);
+          for (int j = 0; j < 2; ++j)  // a super-block's chain starts from zero
+            d1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], p == 0 && kk == 0 ? zero16 : d1[i][j], 0, 0, 0);
       }
       if (p == 3) {
         // super-block end: min term on the bf16 matrix cores (k positions
@@ -255,18 +293,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* 
             sa[pl] = __builtin_bit_cast(g2_bf16x8, lane < 32 ? Ss[par][pl][wm * 64 + 32 * i + fr] : z);
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            g2_f32x16 d2;
+            // D1 is consumed first, then its registers hold D2
 #pragma unroll
-            for (int v = 0; v < 16; ++v) d2[v] = 0.f;
-            d2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sa[2], bm[j], d2, 0, 0, 0);
-            d2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sa[1], bm[j], d2, 0, 0, 0);
-            d2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sa[0], bm[j], d2, 0, 0, 0);
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf(dd[j], d1[i][j][v], acc[i][j][v]);
+            d1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sa[2], bm[j], zero16, 0, 0, 0);
+            d1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sa[1], bm[j], d1[i][j], 0, 0, 0);
+            d1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sa[0], bm[j], d1[i][j], 0, 0, 0);
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              acc[i][j][v] = fmaf(dd[j], d1[i][j][v], acc[i][j][v]);
-              acc[i][j][v] = fmaf(-dm[j], d2[v], acc[i][j][v]);
-              d1[i][j][v] = 0.f;
-            }
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf(-dm[j], d1[i][j][v], acc[i][j][v]);
           }
         }
       }
@@ -281,6 +315,15 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* 
     for (int v = 0; v < 16; ++v) {
       const int m = m0 + wm * 64 + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
       if (m >= M) continue;
+      if (part) {
+        float* pr = part + ((size_t)split * M + m) * N;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = n0 + wn * 64 + 32 * j + fr;
+          if (n < N) pr[n] = acc[i][j][v];
+        }
+        continue;
+      }
       const float rs = ws.rsc[m];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -290,27 +333,90 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* 
     }
 }
 
-// Whether the 256 x 128 tiling fills the GPU for this shape (enough
-// workgroups for three quarters of the CUs); otherwise gemm_q4k.h's 64-token
-// tiles give more parallelism (measured on MI355X: 14336 x 4096 at M = 512
-// 122 us here vs 176 us; 4096 x 14336 at M = 512, 64 workgroups, 336 us here
-// vs 209 us there).
-inline bool gemm_q4k2_fits(int m, int n) {
-  return (int64_t)((m + 255) / 256) * ((n + 127) / 128) * 4 >= (int64_t)device_cus() * 3;
+// y[m, n] = (sum over s in order of part[s][m][n]) * 2^t_m + bias[n]: one
+// thread per output, fixed summation order (the result does not depend on
+// which split finished first).
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __restrict__ part, int splits, int M,
+                                                                int N, const float* __restrict__ rsc,
+                                                                const float* __restrict__ bias,
+                                                                float* __restrict__ y) {
+  const size_t total = (size_t)M * N;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int m = (int)(i / (size_t)N), n = (int)(i - (size_t)m * N);
+  float acc = part[i];
+  for (int s = 1; s < splits; ++s) acc += part[(size_t)s * total + i];
+  y[i] = acc * rsc[m] + (bias ? bias[n] : 0.f);
 }
 
-// Launches the activation prep and the GEMM; `workspace` holds
-// gemm_q4k_ws_layout(m, k) bytes.
+// Split-K plan of the 256 x 128 tiling for an M x N x K problem: `splits`
+// workgroups per output tile so that the grid fills the GPU; 0 when the
+// tiling should not be used (gemm_q4k.h's 64-token tiles are faster).
+// Measured on MI355X (this tiling vs gemm_q4k.h): 14336 x 4096 at M = 512
+// (224 tiles, unsplit) 111 vs 177 us; 4096 x 14336 at M = 512 (64 tiles) 285
+// vs 209 us unsplit, 110 us in four splits; M = 64 of 4096 x 14336 in eight
+// splits 54 vs 190 us.
+struct GemmQ4k2Plan {
+  int splits = 0;  // 0: not this kernel; 1: no partial sums
+  int sbps = 0;    // super-blocks per split
+  size_t part_bytes = 0;
+};
+
+// Workspace bytes the split-K partial sums of an M-row problem may need
+// beyond gemm_q4k_ws_layout: splits are only planned while the tile count
+// times the splits stays within the CU count, so S x N <= 128 x CUs / tiles_m.
+// The bound is taken at 256 CUs (MI355X), independent of the device present:
+// on a device with more CUs the splits are capped by the space given.
+inline size_t gemm_q4k2_part_bound(int64_t m) {
+  const int64_t tiles_m = (m + 255) / 256;
+  if (tiles_m > 4) return 0;  // M > 1024: enough tiles without splitting
+  return (size_t)m * 128 * (size_t)(256 / tiles_m) * 4;
+}
+
+inline GemmQ4k2Plan gemm_q4k2_plan(int m, int n, int k, size_t part_avail) {
+  GemmQ4k2Plan pl;
+  if ((int64_t)m * k * 2 >= (int64_t(1) << 31)) return pl;  // 32-bit buffer offsets
+  const int64_t tiles = (int64_t)((m + 255) / 256) * ((n + 127) / 128);
+  const int64_t cus = device_cus();
+  if (tiles * 4 >= cus * 3) {
+    pl.splits = 1;
+    pl.sbps = k / 256;
+    return pl;
+  }
+  const int sbs = k / 256;
+  int splits = (int)std::min<int64_t>(cus / tiles, sbs / 2);  // at least two super-blocks per split
+  const size_t per = (size_t)m * n * 4;
+  if (per > 0) splits = (int)std::min<size_t>((size_t)splits, part_avail / per);
+  // split unless gemm_q4k.h's 64-token tiles give more than twice the
+  // workgroups (a workgroup here does four times their work per step, at
+  // about twice their speed)
+  const int64_t tiles_64 = (int64_t)((m + 63) / 64) * ((n + 127) / 128);
+  if (splits < 2 || 2 * tiles * splits < tiles_64) return pl;
+  pl.sbps = (sbs + splits - 1) / splits;
+  pl.splits = (sbs + pl.sbps - 1) / pl.sbps;
+  pl.part_bytes = (size_t)pl.splits * per;
+  return pl;
+}
+
+// Launches the activation prep and the GEMM (and, split, the reduction);
+// `workspace` holds gemm_q4k_ws_layout(m, k) bytes followed by
+// plan.part_bytes.
 inline int launch_gemm_q4k2(const void* w, const void* x, const float* bias, float* y, int m, int n, int k,
-                            void* workspace, hipStream_t s) {
+                            void* workspace, const GemmQ4k2Plan& plan, hipStream_t s) {
   GemmQ4kWs ws;
-  gemm_q4k_ws_layout(m, k, static_cast<char*>(workspace), &ws);
+  const size_t base = gemm_q4k_ws_layout(m, k, static_cast<char*>(workspace), &ws);
+  float* part = plan.splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + base) : nullptr;
   hipLaunchKernelGGL(gemm_prep_kernel, dim3((unsigned)m), dim3(256), 0, s, static_cast<const uint16_t*>(x), m, k, ws);
   if (int rc = check_launch("gemm_prep")) return rc;
-  const int tiles_n = (n + 127) / 128, tiles_m = (m + 255) / 256;
-  hipLaunchKernelGGL((gemm_q4k2_kernel<4, 2>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, s,
-                     static_cast<const uint8_t*>(w), ws, bias, y, m, n, k, tiles_m);
-  return check_launch("gemm_q4k2");
+  const int tiles_n = (n + 127) / 128, tiles_m = (m + 255) / 256, tiles = tiles_m * tiles_n;
+  hipLaunchKernelGGL((gemm_q4k2_kernel<4, 2>), dim3((unsigned)(tiles * plan.splits)), dim3(512), 0, s,
+                     static_cast<const uint8_t*>(w), ws, bias, y, m, n, k, tiles_m, tiles, plan.sbps, part);
+  if (int rc = check_launch("gemm_q4k2")) return rc;
+  if (!part) return 0;
+  const size_t total = (size_t)m * n;
+  hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part,
+                     plan.splits, m, n, ws.rsc, bias, y);
+  return check_launch("gemm_split_reduce");
 }
 
 }  // namespace draco

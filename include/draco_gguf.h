@@ -141,8 +141,11 @@ int draco_gguf_gemv_residual(int ggml_type, const void* w, size_t w_bytes, const
 /*
  * Workspace bytes draco_gguf_gemm / draco_gguf_linear use for m token rows of
  * length k with this weight type (0 when the type's GEMM needs none).  Q4_K
- * takes m * k * 2 + 3 * m * (k / 32) * 2 + m * 4 bytes (rounded up to 256 per
- * part): the activations as float16 and their 32-element sums.
+ * requires m * k * 2 + 3 * m * (k / 32) * 2 + m * 4 bytes (rounded up to 256
+ * per part: the activations as float16, their 32-element sums, the row
+ * scales); for m <= 1024 the size returned adds m * 128 * (256 / ceil(m /
+ * 256)) * 4 bytes of room for split-K partial sums, which shapes with too few
+ * output tiles to fill the GPU use when the workspace given holds them.
  */
 size_t draco_gguf_gemm_workspace_size(int ggml_type, int64_t m, int64_t k);
 
@@ -151,10 +154,12 @@ size_t draco_gguf_gemm_workspace_size(int ggml_type, int64_t m, int64_t k);
  * float32 accumulate and output):
  *   y[m, n] = x_bf16[m, k] . W[n, k]^T (+ bias[n]),  m >= 1.
  * Same reference call sites as draco_gguf_gemv, for prompt-sized M.
- * `workspace` (device memory, workspace_bytes >= draco_gguf_gemm_workspace_size)
- * selects the float16 matrix-core kernel for Q4_K; NULL runs the
- * workspace-free kernel (three bf16 weight planes, slower).  A workspace that
- * is given but too small is an error (DRACO_EWORKSPACE).
+ * `workspace` (device memory, 256-byte aligned, workspace_bytes =
+ * draco_gguf_gemm_workspace_size) selects the float16 matrix-core kernels for
+ * Q4_K; NULL runs the workspace-free kernel (three bf16 weight planes,
+ * slower).  A workspace below the required part (the size without the
+ * split-K room) is an error (DRACO_EWORKSPACE); one without the room runs
+ * unsplit.
  */
 int draco_gguf_gemm(int ggml_type, const void* w, size_t w_bytes, const void* x_bf16, const float* bias, float* y,
                     int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes, void* stream);

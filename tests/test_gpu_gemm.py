@@ -86,6 +86,35 @@ def test_gemm_q4k_without_workspace_matches():
     assert gemm_workspace_bytes(Q4_K, m, k) > 0
 
 
+def _q4k_ws_required(m, k):
+    al = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    return al(m * k * 2) + al(3 * m * (k // 32) * 2) + al(m * 4)
+
+
+@pytest.mark.parametrize("n,k,m", [(1000, 4096, 200), (4096, 14336, 64)])
+def test_gemm_q4k_split_k(n, k, m):
+    """Few output tiles: the workspace's split-K room splits the K range over
+    several workgroups per tile, and a second launch adds their partial sums in
+    split order (bit-identical from run to run); a workspace without the room
+    runs unsplit.  Both agree with the oracle."""
+    blocks, w = quantized(Q4_K, n, k, 21)
+    x = activations(m, k, 21, torch.bfloat16).cuda()
+    wq = torch.from_numpy(blocks).cuda()
+    b = torch.from_numpy(np.random.default_rng(21).standard_normal(n, dtype=np.float32)).cuda()
+    full = gemm_workspace_bytes(Q4_K, m, k)
+    assert full > _q4k_ws_required(m, k)
+    print(f"gemm Q4_K split-K [{n},{k}] m={m}", flush=True)
+    ws = torch.empty(full, dtype=torch.uint8, device="cuda")
+    y1 = gguf_gemm(x, wq, Q4_K, (n, k), bias=b, workspace=ws).cpu()
+    y2 = gguf_gemm(x, wq, Q4_K, (n, k), bias=b, workspace=ws).cpu()
+    assert torch.equal(y1, y2)
+    ws_min = torch.empty(_q4k_ws_required(m, k), dtype=torch.uint8, device="cuda")
+    y3 = gguf_gemm(x, wq, Q4_K, (n, k), bias=b, workspace=ws_min).cpu()
+    ref = matmul_ref.linear_ref(x.cpu().float().numpy(), w) + b.cpu().numpy()
+    check_close(y1.numpy(), ref, f"gemm Q4_K split-K [{n},{k}] m={m}")
+    check_close(y3.numpy(), ref, f"gemm Q4_K unsplit [{n},{k}] m={m}")
+
+
 def test_gemm_q4k_m2048_bias_via_linear():
     blocks, w = quantized(Q4_K, 1024, 2048, 13)
     x = activations(2048, 2048, 13, torch.bfloat16)

@@ -1,0 +1,255 @@
+// Small-batch decode GEMV (2..16 activation rows) for Q4_K with the weight
+// tiles staged through LDS.
+//
+// The chunk math is the persistent matrix-core GEMV's (gemv_mfma.h:
+// activations resident in registers for the launch, wave ks taking chunks
+// ks, ks + W, ...; one v_mfma_f32_16x16x32_bf16 per 32-weight group against
+// the codes as 128 + code, the group sums from one more MFMA, scales on the
+// VALU), and so are the results, bit for bit.  The weights reach the lanes
+// differently.  A lane's share of a 16-row tile in the MFMA layout is four
+// 8-byte pieces per chunk spread over 16 rows; loading that straight into
+// registers issues requests that each touch 16 rows (measured on MI355X:
+// with the math removed, a 2 x 14336 x 4096 launch moved 2.9 TB/s where a
+// plain read of the same bytes reaches 5.3).  Here the 16 rows of a tile,
+// one contiguous span of 16 x row_bytes, are read by the whole workgroup as
+// consecutive 16-byte pieces (piece p by thread p mod 512), written to an
+// LDS image with each row padded by 16 bytes (rows fall on different
+// banks), and the lanes read their pieces from there (4.4 TB/s with the
+// math removed).  One tile is in flight while the previous one is
+// multiplied: tile i + 2 is requested right after tile i + 1 is written to
+// LDS, two barriers per tile.
+#pragma once
+
+#include "gemv_mfma.h"
+
+namespace draco {
+
+constexpr int kMflMaxRowBytes = 16 * 144;  // Q4_K rows of K <= 4096
+
+// LDS bytes of one matrix's tile image for this row length.
+__host__ __device__ constexpr int mfl_tile_lds(int row_bytes) { return 16 * (row_bytes + 16); }
+
+// Streams ntiles 16-row tiles of NR Q4_K matrices through the LDS image `wl`
+// (NR x mfl_tile_lds(row_bytes) bytes) against the wave's resident
+// activations xr.  tile_base(i, r) gives matrix r's buffer resource and the
+// byte offset of tile i's first row; emit(i, tot) runs on wave 0 with tile
+// i's summed 16 x 16 result.
+template <int NR, int W, class TileBase, class Emit>
+__device__ __forceinline__ void mfl_stream_q4k(const typename MfpTypes<kQ4_K>::X (&xr)[16 / W], int chunks,
+                                               int ntiles, int row_bytes, TileBase tile_base, Emit emit,
+                                               uint8_t* __restrict__ wl, mf_f32x4 (&part)[W][NR][64]) {
+  constexpr int NT = W * 64, CPW = 16 / W;
+  constexpr int PPT = (kMflMaxRowBytes + NT - 1) / NT;  // pieces per thread: 16 x row_bytes / 16 bytes
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4, nl = lane & 15;
+  const int rs_bytes = row_bytes + 16, img = 16 * rs_bytes;
+  const int ppr = row_bytes >> 4, pieces = row_bytes;  // pieces per row, per tile
+
+  // this thread's pieces: the same LDS destinations for every tile
+  int dst[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    const int pc = tid + NT * j;
+    const int row = pc / ppr;
+    dst[j] = pc < pieces ? row * rs_bytes + ((pc - row * ppr) << 4) : -1;
+  }
+  uint4 stg[NR][PPT];
+  // offsets past the end of a resource read zero without touching memory
+  auto issue = [&](int i) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const MfRow t = tile_base(min(i, ntiles - 1), r);
+      const __amdgpu_buffer_rsrc_t rs = i < ntiles ? t.rs : make_rsrc(nullptr, 0u);
+#pragma unroll
+      for (int j = 0; j < PPT; ++j) {
+        const int pc = tid + NT * j;
+        const uint32_t off = pc < pieces ? (uint32_t)t.rowoff + ((uint32_t)pc << 4) : 0x80000000u;
+        typedef int v4i __attribute__((ext_vector_type(4)));
+        const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+        stg[r][j] = uint4{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+      }
+    }
+  };
+  auto commit = [&]() {
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int j = 0; j < PPT; ++j)
+        if (dst[j] >= 0) *reinterpret_cast<uint4*>(wl + r * img + dst[j]) = stg[r][j];
+  };
+
+  if (ntiles <= 0) return;
+  issue(0);
+  commit();
+  issue(1);
+  __syncthreads();
+  for (int i = 0; i < ntiles; ++i) {
+    mf_f32x4 acc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const int cc = ks + W * j;
+      if (cc < chunks) {
+        MfChunk<kQ4_K> wc[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const uint8_t* rp = wl + r * img + nl * rs_bytes + cc * 144;
+          wc[r].head = *reinterpret_cast<const uint4*>(rp);
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const uint2 t = *reinterpret_cast<const uint2*>(rp + 16 + 32 * p + 8 * q);
+            wc[r].qs[p][0] = t.x;
+            wc[r].qs[p][1] = t.y;
+          }
+        }
+        mf_chunk_q4<kQ4_K, true, NR>(xr[j], wc, q, acc);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) part[ks][r][lane] = acc[r];
+    __syncthreads();  // tile i read by every wave, its partial tiles written
+    if (ks == 0) {
+      mf_f32x4 tot[NR];
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        tot[r] = part[0][r][lane];
+#pragma unroll
+        for (int w = 1; w < W; ++w) {
+          const mf_f32x4 pp = part[w][r][lane];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) tot[r][v] += pp[v];
+        }
+      }
+      emit(i, tot);
+    }
+    if (i + 1 < ntiles) {
+      commit();      // tile i + 1
+      issue(i + 2);  // an empty resource past the last tile
+    }
+    __syncthreads();  // tile i + 1 in LDS, the partial tiles free again
+  }
+}
+
+// The decode GEMV of 2..16 bf16 token rows over Q4_K matrices with K <= 4096
+// (gemv_mfp_kernel's jobs, modes and results).
+template <int MODE, int W>
+__global__ __launch_bounds__(W * 64) void gemv_mfl_kernel(StreamJob job) {
+  constexpr int NR = MODE == kSwiGLU ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) uint8_t wl[NR * mfl_tile_lds(kMflMaxRowBytes)];
+  __shared__ mf_f32x4 part[W][NR][64];
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, nl = lane & 15;
+  const int k = job.k, M = job.m;
+  const int chunks = k >> 8;
+  const int ntiles = job.rows >> 4;
+  const int my_tiles = ntiles > (int)blockIdx.x ? (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+
+  typename MfpTypes<kQ4_K>::X xr[16 / W];
+  mfp_load_x<kQ4_K, W>(static_cast<const uint16_t*>(job.x) + (size_t)min(nl, M - 1) * k, chunks, ks, q, xr);
+
+  int c1 = INT_MAX, c2 = INT_MAX, c3 = INT_MAX;
+  if constexpr (MODE == kPlain) {
+    if (job.n_mats > 1) c1 = job.n[0];
+    if (job.n_mats > 2) c2 = c1 + job.n[1];
+    if (job.n_mats > 3) c3 = c2 + job.n[2];
+  }
+  const uint8_t *w0 = job.w[0], *w1 = job.w[1], *w2 = job.w[2], *w3 = job.w[3];
+  const int n0 = job.n[0], n1 = job.n[1], n2 = job.n[2], n3 = job.n[3];
+  float *y0 = job.y[0], *y1 = job.y[1], *y2 = job.y[2], *y3 = job.y[3];
+  uint16_t *b0 = job.yb[0], *b1 = job.yb[1], *b2 = job.yb[2], *b3 = job.yb[3];
+  float* const resid = job.resid;
+  uint16_t* const resid_bf16 = job.resid_bf16;
+  const float* const bias = job.bias;
+  const int row_bytes = job.row_bytes;
+  auto pick = [](int mat, auto v0, auto v1, auto v2, auto v3) {
+    auto v = v0;
+    v = mat >= 1 ? v1 : v;
+    v = mat >= 2 ? v2 : v;
+    v = mat >= 3 ? v3 : v;
+    return v;
+  };
+  auto locate = [=](int row, int& mat, int& lrow) {
+    mat = 0;
+    lrow = row;
+    if constexpr (MODE == kPlain) {
+      mat = (row >= c1) + (row >= c2) + (row >= c3);
+      int base = row >= c1 ? c1 : 0;
+      base = row >= c2 ? c2 : base;
+      base = row >= c3 ? c3 : base;
+      lrow = row - base;
+    }
+  };
+  auto tile_base = [=](int i, int r) {
+    int mat, lrow;
+    locate(16 * ((int)blockIdx.x + i * (int)gridDim.x), mat, lrow);
+    const int mm = NR == 2 ? r : mat;
+    const uint8_t* wp = pick(mm, w0, w1, w2, w3);
+    const int nn = pick(mm, n0, n1, n2, n3);
+    return MfRow{make_rsrc(wp, (uint32_t)((int64_t)nn * row_bytes)), lrow * row_bytes};
+  };
+  auto emit = [=](int i, const mf_f32x4 (&tot)[NR]) {
+    int omat, olrow;
+    locate(16 * ((int)blockIdx.x + i * (int)gridDim.x) + nl, omat, olrow);
+    const int n = pick(omat, n0, n1, n2, n3);
+    float* const yp = pick(omat, y0, y1, y2, y3);
+    uint16_t* const ybp = pick(omat, b0, b1, b2, b3);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 4 * q + v;  // D layout: lane l holds rows 4 (l / 16) + v, column l % 16
+      if (m >= M) continue;
+      const size_t o = (size_t)m * n + olrow;
+      if constexpr (MODE == kResid) {
+        const float out = resid[o] + tot[0][v];
+        resid[o] = out;
+        if (resid_bf16) resid_bf16[o] = f32_to_bf16_rne(out);
+      } else {
+        float out = tot[0][v];
+        if constexpr (MODE == kSwiGLU) out = silu(tot[0][v]) * tot[1][v];
+        if (MODE == kPlain && bias) out += bias[olrow];
+        if (yp) yp[o] = out;
+        if (ybp) ybp[o] = f32_to_bf16_rne(out);
+      }
+    }
+  };
+  mfl_stream_q4k<NR, W>(xr, chunks, my_tiles, row_bytes, tile_base, emit, wl, part);
+}
+
+template <int MODE, int W>
+static int launch_gemv_mfl(const StreamJob& job, int blocks_per_cu, hipStream_t s) {
+  if (job.k > 4096 || job.k % 256 != 0 || job.rows % 16 != 0)
+    return set_error(DRACO_EINVAL_SHAPE, "LDS-staged matrix-core GEMV takes K <= 4096 and whole 16-row tiles");
+  const int tiles = job.rows / 16;
+  const int blocks = std::max(1, std::min(tiles, device_cus() * blocks_per_cu));
+  hipLaunchKernelGGL((gemv_mfl_kernel<MODE, W>), dim3(blocks), dim3(W * 64), 0, s, job);
+  return check_launch("gemv_mfl");
+}
+
+template <int MODE>
+static int gemv_mfma_dispatch(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s) {
+  // bf16 rows of at most 16 chunks: the persistent form (activations resident
+  // in registers), one 512-thread workgroup per CU (measured best: 14336 x 4096
+  // Q4_K at M = 16 18 us vs 30 us for the one-tile-per-workgroup form)
+  // (SwiGLU's two weight sets fit the 512-thread register budget for Q4_K only)
+  if (xbf16 && job.k <= 4096 && (MODE != kSwiGLU || qtype == kQ4_K)) {
+    if constexpr (MODE != kSwiGLU) {
+      if (qtype == kQ6_K)
+        return d_last ? launch_gemv_mfp<kQ6_K, true, MODE, 8>(job, 1, s)
+                      : launch_gemv_mfp<kQ6_K, false, MODE, 8>(job, 1, s);
+    }
+    // Q4_K: the LDS-staged form above, bit-identical and faster (measured at
+    // 16 rows: gate/up 33.1 -> 28.4 us, q/k/v 12.6 -> 11.5, o 11.1 -> 9.6)
+    if (qtype == kQ4_K) return launch_gemv_mfl<MODE, 8>(job, 1, s);
+    if constexpr (MODE != kSwiGLU) return launch_gemv_mfp<kQ4_0, false, MODE, 8>(job, 1, s);
+  }
+  if (qtype == kQ6_K)
+    return d_last ? launch_gemv_mfma<kQ6_K, true, true, MODE>(job, s) : launch_gemv_mfma<kQ6_K, false, true, MODE>(job, s);
+  if (qtype == kQ4_K)
+    return xbf16 ? launch_gemv_mfma<kQ4_K, false, true, MODE>(job, s)
+                 : launch_gemv_mfma<kQ4_K, false, false, MODE>(job, s);
+  return xbf16 ? launch_gemv_mfma<kQ4_0, false, true, MODE>(job, s) : launch_gemv_mfma<kQ4_0, false, false, MODE>(job, s);
+}
+
+}  // namespace draco

@@ -704,27 +704,4 @@ static int launch_gemv_mfma(const StreamJob& job, hipStream_t s) {
   return check_launch("gemv_mfma");
 }
 
-template <int MODE>
-static int gemv_mfma_dispatch(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s) {
-  // bf16 rows of at most 16 chunks: the persistent form (activations resident
-  // in registers), one 512-thread workgroup per CU (measured best: 14336 x 4096
-  // Q4_K at M = 16 18 us vs 30 us for the one-tile-per-workgroup form)
-  // (SwiGLU's two weight sets fit the 512-thread register budget for Q4_K only)
-  if (xbf16 && job.k <= 4096 && (MODE != kSwiGLU || qtype == kQ4_K)) {
-    if constexpr (MODE != kSwiGLU) {
-      if (qtype == kQ6_K)
-        return d_last ? launch_gemv_mfp<kQ6_K, true, MODE, 8>(job, 1, s)
-                      : launch_gemv_mfp<kQ6_K, false, MODE, 8>(job, 1, s);
-    }
-    if (qtype == kQ4_K) return launch_gemv_mfp<kQ4_K, false, MODE, 8>(job, 1, s);
-    if constexpr (MODE != kSwiGLU) return launch_gemv_mfp<kQ4_0, false, MODE, 8>(job, 1, s);
-  }
-  if (qtype == kQ6_K)
-    return d_last ? launch_gemv_mfma<kQ6_K, true, true, MODE>(job, s) : launch_gemv_mfma<kQ6_K, false, true, MODE>(job, s);
-  if (qtype == kQ4_K)
-    return xbf16 ? launch_gemv_mfma<kQ4_K, false, true, MODE>(job, s)
-                 : launch_gemv_mfma<kQ4_K, false, false, MODE>(job, s);
-  return xbf16 ? launch_gemv_mfma<kQ4_0, false, true, MODE>(job, s) : launch_gemv_mfma<kQ4_0, false, false, MODE>(job, s);
-}
-
 }  // namespace draco

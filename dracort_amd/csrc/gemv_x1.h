@@ -30,7 +30,7 @@
 
 #include <climits>
 
-#include "gemv_mfma.h"
+#include "gemv_mfl.h"
 #include "gemv_stream.h"
 
 namespace draco {

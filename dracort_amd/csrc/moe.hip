@@ -27,7 +27,7 @@
 // of once per token row of the register core.
 #include "draco_internal.h"
 #include "gemv_core.h"
-#include "gemv_mfma.h"
+#include "gemv_mfl.h"
 
 namespace draco {
 
@@ -283,11 +283,12 @@ __global__ __launch_bounds__(256) void moe_up_mfma_kernel(ExpertPtrs wg, ExpertP
 // grid (workgroups per expert, experts); for each 16-token tile of its
 // expert a workgroup loads the gathered activations into registers once
 // (eight waves split the hidden dimension) and streams its share of the
-// gate/up row tiles against them (mfp_stream).
+// gate/up row tiles against them through LDS (mfl_stream_q4k).
 __global__ __launch_bounds__(512) void moe_up_mfp_kernel(ExpertPtrs wg, ExpertPtrs wu,
                                                          const uint16_t* __restrict__ x, int H, int I, MoeWs ws) {
   constexpr int W = 8;
-  __shared__ mf_f32x4 part[2][W][2][64];
+  __shared__ __attribute__((aligned(16))) uint8_t wl[2 * mfl_tile_lds(kMflMaxRowBytes)];
+  __shared__ mf_f32x4 part[W][2][64];
   const int e = blockIdx.y;
   const int cnt = ws.counts[e];
   if (cnt == 0) return;
@@ -309,9 +310,9 @@ __global__ __launch_bounds__(512) void moe_up_mfp_kernel(ExpertPtrs wg, ExpertPt
     const int tok = ws.assign_tok[off + t0 + min(nl, mt - 1)];
     typename MfpTypes<kQ4_K>::X xr[16 / W];
     mfp_load_x<kQ4_K, W>(x + (size_t)tok * H, chunks, ks, q, xr);
-    auto tile_rsrc = [=](int i, int r) {
+    auto tile_base = [=](int i, int r) {
       const int row = 16 * ((int)blockIdx.x + i * (int)gridDim.x);
-      return MfRow{make_rsrc(r == 0 ? gp : upp, mat_bytes), (row + nl) * row_bytes};
+      return MfRow{make_rsrc(r == 0 ? gp : upp, mat_bytes), row * row_bytes};
     };
     auto emit = [=](int i, const mf_f32x4 (&tot)[2]) {
       const int col = 16 * ((int)blockIdx.x + i * (int)gridDim.x) + nl;
@@ -328,7 +329,7 @@ __global__ __launch_bounds__(512) void moe_up_mfp_kernel(ExpertPtrs wg, ExpertPt
         }
       }
     };
-    mfp_stream<kQ4_K, false, 2, W>(xr, chunks, my_tiles, make_rsrc(gp, 0u), tile_rsrc, emit, part);
+    mfl_stream_q4k<2, W>(xr, chunks, my_tiles, row_bytes, tile_base, emit, wl, part);
   }
 }
 

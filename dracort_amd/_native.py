@@ -31,7 +31,7 @@ DRACO_GGUF_GGML_ORDER = 0x100  # Q2_K / Q3_K / Q6_K in upstream ggml field order
 DRACO_GGUF_Q6K_D_LAST = DRACO_GGUF_GGML_ORDER
 DRACO_GGUF_NOALLOC_SCRATCH_BYTES = 64 << 20
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _c_int, _c_i64, _c_size, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
 
@@ -49,6 +49,9 @@ SIGNATURES = {
     ),
     "draco_gguf_gemv_swiglu": (_c_int, [_c_int, _vp, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "draco_gguf_gemv_residual": (_c_int, [_c_int, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
+    "draco_gguf_gemv_residual_workspace_size": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64]),
+    "draco_gguf_gemv_residual_ws": (_c_int, [_c_int, _vp, _c_size, _vp, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
+                                             _vp, _c_size, _vp]),
     "draco_gguf_gemm_workspace_size": (_c_size, [_c_int, _c_i64, _c_i64]),
     "draco_gguf_gemm": (_c_int, [_c_int, _vp, _c_size, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_size, _vp]),
     "draco_gguf_linear": (

@@ -137,7 +137,7 @@ using namespace draco;
 
 extern "C" {
 
-int draco_gguf_abi_version(void) { return 3; }
+int draco_gguf_abi_version(void) { return 4; }
 
 const char* draco_gguf_last_error(void) { return g_last_error; }
 
@@ -251,8 +251,9 @@ int draco_gguf_gemv_swiglu(int ggml_type, const void* w_gate, const void* w_up, 
                               x_dtype == DRACO_DTYPE_BF16, (int)m, (int)n, (int)k, static_cast<hipStream_t>(stream));
 }
 
-int draco_gguf_gemv_residual(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype, float* resid,
-                             void* resid_bf16, int64_t m, int64_t n, int64_t k, void* stream) {
+static int gemv_residual_impl(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype, float* resid,
+                              void* resid_bf16, int64_t m, int64_t n, int64_t k, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   g_last_error[0] = 0;
   TypeInfo t;
   if (int rc = decode_type(ggml_type, &t)) return rc;
@@ -270,9 +271,29 @@ int draco_gguf_gemv_residual(int ggml_type, const void* w, size_t w_bytes, const
   const size_t xbytes = (size_t)m * k * (x_dtype == DRACO_DTYPE_BF16 ? 2 : 4);
   if (overlaps(x, xbytes, resid, (size_t)m * n * 4) || overlaps(x, xbytes, resid_bf16, (size_t)m * n * 2))
     return set_error(DRACO_EINVAL_ARG, "x overlaps resid / resid_bf16");
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 255u))
+    return set_error(DRACO_EINVAL_ARG, "GEMV workspace must be 256-byte aligned");
   return gemv_resid_dispatch(t.base, t.d_last, w, x, x_dtype == DRACO_DTYPE_BF16, resid,
-                             static_cast<uint16_t*>(resid_bf16), (int)m, (int)n, (int)k,
-                             static_cast<hipStream_t>(stream));
+                             static_cast<uint16_t*>(resid_bf16), (int)m, (int)n, (int)k, workspace,
+                             workspace ? workspace_bytes : 0, static_cast<hipStream_t>(stream));
+}
+
+int draco_gguf_gemv_residual(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype, float* resid,
+                             void* resid_bf16, int64_t m, int64_t n, int64_t k, void* stream) {
+  return gemv_residual_impl(ggml_type, w, w_bytes, x, x_dtype, resid, resid_bf16, m, n, k, nullptr, 0, stream);
+}
+
+size_t draco_gguf_gemv_residual_workspace_size(int ggml_type, int64_t m, int64_t n, int64_t k) {
+  TypeInfo t;
+  if (decode_type(ggml_type, &t) || m < 1 || m > 16 || n < 1 || k < 1 || n > kMaxDim || k > kMaxDim) return 0;
+  return gemv_resid_split_bytes(t.base, (int)m, (int)n, (int)k);
+}
+
+int draco_gguf_gemv_residual_ws(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype,
+                                float* resid, void* resid_bf16, int64_t m, int64_t n, int64_t k, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  return gemv_residual_impl(ggml_type, w, w_bytes, x, x_dtype, resid, resid_bf16, m, n, k, workspace,
+                            workspace_bytes, stream);
 }
 
 // shared checks of the fused-RMSNorm entry points: x [m, k] float32, norm_w [k], x_norm [m, k] bf16

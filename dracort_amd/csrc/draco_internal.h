@@ -34,8 +34,11 @@ int gemv_multi_dispatch(int qtype, bool d_last, int n_mats, const void* const* w
 int gemv_swiglu_dispatch(int qtype, bool d_last, const void* w_gate, const void* w_up, float* y, uint16_t* yb,
                          const void* x, bool xbf16, int m, int n, int k, hipStream_t s);
 
+// workspace: NULL, or room for the split-K partial sums (gemv_resid_split_bytes)
+size_t gemv_resid_split_bytes(int qtype, int m, int n, int k);
 int gemv_resid_dispatch(int qtype, bool d_last, const void* w, const void* x, bool xbf16, float* resid,
-                        uint16_t* resid_bf16, int m, int n, int k, hipStream_t s);
+                        uint16_t* resid_bf16, int m, int n, int k, void* workspace, size_t workspace_bytes,
+                        hipStream_t s);
 
 // RMSNorm of m rows of n float32 values into float32 y and / or bf16 yb.
 int rms_norm_launch(const float* x, const float* w, float eps, float* y, uint16_t* yb, int64_t m, int64_t n,

@@ -407,16 +407,25 @@ __global__ __launch_bounds__(TPW * KS * 64) void gemv_mfma_kernel(StreamJob job)
     const int mm = NR == 2 ? r : mat;
     rs[r] = make_rsrc(job.w[mm], (uint32_t)((int64_t)job.n[mm] * job.row_bytes));
   }
-  const int rowoff = (int)((int64_t)min(lrow0 + nl, job.n[NR == 2 ? 0 : mat] - 1) * job.row_bytes);
+  // this workgroup's chunks: all, or split blockIdx.y's range
+  constexpr int kChunkBytes = Fmt<QT>::BYTES * (256 / Fmt<QT>::QK);
+  int c0 = 0, nch = chunks;
+  if (job.part) {
+    c0 = (int)blockIdx.y * job.split_chunks;
+    nch = min(job.split_chunks, chunks - c0);
+  }
+  const int rowoff =
+      (int)((int64_t)min(lrow0 + nl, job.n[NR == 2 ? 0 : mat] - 1) * job.row_bytes) + c0 * kChunkBytes;
 
   mf_f32x4 acc[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) acc[r] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
-  const void* xrow = static_cast<const uint8_t*>(job.x) + (size_t)min(nl, M - 1) * k * (XBF16 ? 2 : 4);
+  const void* xrow =
+      static_cast<const uint8_t*>(job.x) + ((size_t)min(nl, M - 1) * k + (size_t)c0 * 256) * (XBF16 ? 2 : 4);
   if constexpr (QT == kQ6_K)
-    mf_accumulate_q6k<DL, NR, KS>(rs, rowoff, xrow, q, ks, chunks, acc);
+    mf_accumulate_q6k<DL, NR, KS>(rs, rowoff, xrow, q, ks, nch, acc);
   else
-    mf_accumulate<QT, XBF16, NR, false, KS>(rs, rowoff, xrow, q, ks, chunks, acc);
+    mf_accumulate<QT, XBF16, NR, false, KS>(rs, rowoff, xrow, q, ks, nch, acc);
 
   // sum the KS partial tiles
 #pragma unroll
@@ -439,6 +448,15 @@ __global__ __launch_bounds__(TPW * KS * 64) void gemv_mfma_kernel(StreamJob job)
   int omat = 0, olrow = orow;
   if constexpr (MODE == kPlain) row_of(job, orow, omat, olrow);
   const int n = job.n[omat];
+  if constexpr (MODE != kSwiGLU) {
+    if (job.part) {  // one matrix: the split's raw sums
+      float* const pp = job.part + (size_t)blockIdx.y * M * n;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (4 * q + v < M) pp[(size_t)(4 * q + v) * n + olrow] = tot[0][v];
+      return;
+    }
+  }
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int m = 4 * q + v;  // D layout: lane l holds rows 4 (l / 16) + v, column l % 16
@@ -683,6 +701,136 @@ inline bool mfma_gemv_ok(int qtype, const StreamJob& job, bool xbf16) {
   return true;
 }
 
+// The split launch's second half: out = sum over s in order of part[s] (per
+// element), then the mode's epilogue (kResid: resid += out and its bf16 copy;
+// kPlain: y = out + bias).
+template <int MODE>
+__global__ __launch_bounds__(256) void gemv_split_sum_kernel(const float* __restrict__ part, int splits, int M, int n,
+                                                             float* __restrict__ y, uint16_t* __restrict__ yb,
+                                                             const float* __restrict__ bias) {
+  const size_t total = (size_t)M * n;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  float acc = part[i];
+  for (int s = 1; s < splits; ++s) acc += part[(size_t)s * total + i];
+  if constexpr (MODE == kResid) {
+    const float out = y[i] + acc;
+    y[i] = out;
+    if (yb) yb[i] = f32_to_bf16_rne(out);
+  } else {
+    const float out = acc + (bias ? bias[i % (size_t)n] : 0.f);
+    if (y) y[i] = out;
+    if (yb) yb[i] = f32_to_bf16_rne(out);
+  }
+}
+
+// One split of a split-K launch with bf16 activations (Q4_K / Q6_K): grid
+// (tiles, splits), eight waves, wave ks multiplying chunk 8 s + ks of its
+// tile.  The split's activation slab (16 token rows x 8 chunks, 64 KB) is
+// read by the whole workgroup as consecutive 16-byte pieces into LDS (rows
+// padded by 16 bytes) and the lanes take their fragments from there: read
+// straight from global memory, each fragment load touches 16 rows 28 KB
+// apart and the slab's cache lines are fetched several times over.  The
+// wave's weights are requested before the slab is staged.  Stores the raw
+// 16 x 16 sums to part[s]; gemv_split_sum_kernel finishes.  RT row tiles
+// per workgroup share the slab (measured on MI355X, 4096 x 14336 at 16 rows
+// with the sum launch: Q6_K 31.8 / 39.1 / 35.7 us at RT = 1 / 2 / 4, Q4_K
+// 23.6 / 27.7 / 24.2; launched with RT = 1).
+template <int QT, bool DL, int RT = 1>
+__global__ __launch_bounds__(512) void gemv_split_lx_kernel(StreamJob job) {
+  constexpr int XS = 8 * 256 + 8;  // LDS row stride (bf16 elements)
+  __shared__ __attribute__((aligned(16))) uint16_t xs[16 * XS];
+  __shared__ mf_f32x4 part[8][RT][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4, nl = lane & 15;
+  const int k = job.k, M = job.m, chunks = k >> 8;
+  const int s = blockIdx.y, c0 = 8 * s, nch = min(8, chunks - c0);
+  const int row0 = (int)blockIdx.x * 16 * RT;
+  const int n = job.n[0];
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(job.w[0], (uint32_t)((int64_t)n * job.row_bytes));
+  // the wave's chunk of each of its RT row tiles (an empty resource past the
+  // split's last chunk)
+  const int cc = c0 + ks;
+  const __amdgpu_buffer_rsrc_t rw = ks < nch ? rs : make_rsrc(nullptr, 0u);
+  typedef typename MfpTypes<QT>::W WChunk;
+  WChunk wc[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int rowoff = (int)((int64_t)min(row0 + 16 * t + nl, n - 1) * job.row_bytes);
+    if constexpr (QT == kQ6_K)
+      wc[t] = mf_load_q6<DL>(rw, rowoff, min(cc, chunks - 1), q);
+    else
+      wc[t] = mf_load<QT>(rw, rowoff, min(cc, chunks - 1), q);
+  }
+  // the slab: 16 rows x nch * 32 pieces of 16 bytes (rows past M repeat row M - 1)
+  const uint16_t* x = static_cast<const uint16_t*>(job.x);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int pc = tid + 512 * j;
+    const int row = pc >> 8, col = pc & 255;  // 256 pieces per row of 8 chunks
+    if (col < nch * 32) {
+      const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)min(row, M - 1) * k + c0 * 256 + col * 8);
+      *reinterpret_cast<uint4*>(&xs[row * XS + col * 8]) = v;
+    }
+  }
+  __syncthreads();
+  mf_f32x4 acc[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) acc[t] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  if (ks < nch) {
+    const uint16_t* xr = &xs[nl * XS + ks * 256];
+    if constexpr (QT == kQ6_K) {
+      uint2 xf[16];
+#pragma unroll
+      for (int g = 0; g < 16; ++g) xf[g] = *reinterpret_cast<const uint2*>(xr + 16 * g + 4 * q);
+      mf_chunk_q6<RT>(xf, wc, acc);
+    } else {
+      mf_bf16x8 xf[8][1];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) xf[g][0] = *reinterpret_cast<const mf_bf16x8*>(xr + mf_pos<QT>(g, q));
+      mf_chunk_q4<QT, true, RT>(xf, wc, q, acc);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < RT; ++t) part[ks][t][lane] = acc[t];
+  __syncthreads();
+  if (ks >= RT) return;  // wave t < RT sums row tile t
+  const int t = ks;
+  mf_f32x4 tot = part[0][t][lane];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) {
+    const mf_f32x4 pp = part[j][t][lane];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) tot[v] += pp[v];
+  }
+  const int orow = row0 + 16 * t + nl;
+  if (orow >= n) return;
+  float* const pp = job.part + (size_t)s * M * n;
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    if (4 * q + v < M) pp[(size_t)(4 * q + v) * n + orow] = tot[v];
+}
+
+// Splits of a one-matrix matrix-core launch with K > 4096 (one tile per
+// workgroup, eight waves over K) that has fewer tiles than the GPU has CUs
+// four times over: eight chunks per split (one per wave), as many splits as
+// keep the grid within 16 workgroups per CU; 1 = no split.
+inline int gemv_split_count(const StreamJob& job) {
+  const int chunks = job.k >> 8;
+  if (job.n_mats != 1 || job.k <= 4096) return 1;
+  const int64_t tiles = (job.rows + 15) / 16;
+  if (tiles >= (int64_t)device_cus() * 4) return 1;
+  const int s = (chunks + 7) / 8;
+  return tiles * s <= (int64_t)device_cus() * 16 ? s : 1;
+}
+
+// Workspace bytes of a split launch (0: not split).
+inline size_t gemv_split_bytes(const StreamJob& job) {
+  const int s = gemv_split_count(job);
+  return s > 1 ? (size_t)s * job.m * job.n[0] * sizeof(float) : 0;
+}
+
 template <int QT, bool DL, bool XBF16, int MODE>
 static int launch_gemv_mfma(const StreamJob& job, hipStream_t s) {
   const int tiles = (job.rows + 15) / 16;
@@ -694,14 +842,33 @@ static int launch_gemv_mfma(const StreamJob& job, hipStream_t s) {
       return check_launch("gemv_mfma");
     }
   }
+  // split K (job.part set by the caller from gemv_split_bytes): the grid's y
+  // dimension walks the splits, then the ordered sum
+  const int splits = job.part ? (job.k / 256 + job.split_chunks - 1) / job.split_chunks : 1;
   // bf16: eight waves split K (two per SIMD; 4096 x 14336 Q6_K at 16 rows 44.9
   // -> 42.4 us, at 8 rows 37.6 -> 34.6; Q4_K 25.8 -> 24.8); float32 activations
   // need all 512 registers of a lane (one wave per SIMD), so four
-  if constexpr (XBF16)
-    hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 1, 8>), dim3(tiles), dim3(512), 0, s, job);
+  if constexpr (XBF16 && (QT == kQ4_K || QT == kQ6_K)) {
+    if (job.part && job.split_chunks == 8)
+      hipLaunchKernelGGL((gemv_split_lx_kernel<QT, DL>), dim3(tiles, splits), dim3(512), 0, s, job);
+    else
+      hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 1, 8>), dim3(tiles, splits), dim3(512), 0, s, job);
+  } else if constexpr (XBF16)
+    hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 1, 8>), dim3(tiles, splits), dim3(512), 0, s, job);
   else
-    hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 1>), dim3(tiles), dim3(256), 0, s, job);
-  return check_launch("gemv_mfma");
+    hipLaunchKernelGGL((gemv_mfma_kernel<QT, DL, XBF16, MODE, 1>), dim3(tiles, splits), dim3(256), 0, s, job);
+  if (int rc = check_launch("gemv_mfma")) return rc;
+  if constexpr (MODE != kSwiGLU) {
+    if (job.part) {
+      const size_t total = (size_t)job.m * job.n[0];
+      float* const y = MODE == kResid ? job.resid : job.y[0];
+      uint16_t* const yb = MODE == kResid ? job.resid_bf16 : job.yb[0];
+      hipLaunchKernelGGL(gemv_split_sum_kernel<MODE>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                         job.part, splits, job.m, job.n[0], y, yb, job.bias);
+      return check_launch("gemv_split_sum");
+    }
+  }
+  return 0;
 }
 
 }  // namespace draco

@@ -59,6 +59,12 @@ struct StreamJob {
   // bytes between activation rows (0: k elements); set when the launch covers a
   // K window of longer rows (streaming kernel with the activations in LDS only)
   int64_t x_stride;
+  // split K (matrix-core kernel, kPlain / kResid with one matrix): grid.y
+  // workgroups per tile, split s taking chunks [s split_chunks, (s + 1)
+  // split_chunks); each stores its raw 16 x 16 sums to part[s][m][n] and a
+  // second launch adds the splits in order (nullptr: no split)
+  float* part;
+  int split_chunks;
 };
 
 // Row r of this launch -> (matrix, row within it); rows of the matrices of a

@@ -17,6 +17,7 @@ from dracort_amd.kernels.gguf import (  # noqa: F401
     gguf_gemv_multi,
     gguf_gemv_multi_rmsnorm,
     gguf_gemv_residual,
+    gemv_residual_workspace_bytes,
     gguf_gemv_swiglu,
     gguf_gemv_swiglu_rmsnorm,
     gguf_linear,
@@ -33,6 +34,7 @@ __all__ = [
     "gguf_gemv_multi_rmsnorm",
     "gguf_gemv_swiglu_rmsnorm",
     "gguf_gemv_residual",
+    "gemv_residual_workspace_bytes",
     "gguf_gemm",
     "gguf_moe",
     "moe_workspace_bytes",

@@ -318,20 +318,38 @@ def gguf_gemv_residual(
     shape: Tuple[int, int],
     resid: torch.Tensor,
     resid_bf16: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
 ) -> None:
-    """resid += x @ W.T in place (float32); resid_bf16 = bf16(resid) if given."""
+    """resid += x @ W.T in place (float32); resid_bf16 = bf16(resid) if given.
+    ``workspace`` (uint8 device tensor of ``gemv_residual_workspace_bytes``
+    bytes, or None) lets launches with few tiles and long rows split K."""
     n, k = _check_weight(qweight, ggml_type, shape)
     m = _x_rows(x, k)
     _out_check(resid, torch.float32, m * n, "resid")
     _out_check(resid_bf16, torch.bfloat16, m * n, "resid_bf16")
     _same_device(x, qweight, resid)
     lib = _native.load()
+    rb = resid_bf16.data_ptr() if resid_bf16 is not None else None
     with torch.cuda.device(x.device):
-        rc = lib.draco_gguf_gemv_residual(
-            int(ggml_type), qweight.data_ptr(), qweight.numel(), x.data_ptr(), _x_dtype(x), resid.data_ptr(),
-            resid_bf16.data_ptr() if resid_bf16 is not None else None, m, n, k, _stream(x),
-        )
+        if workspace is None:
+            rc = lib.draco_gguf_gemv_residual(
+                int(ggml_type), qweight.data_ptr(), qweight.numel(), x.data_ptr(), _x_dtype(x), resid.data_ptr(),
+                rb, m, n, k, _stream(x),
+            )
+        else:
+            _need_gpu(workspace, "workspace")
+            if workspace.dtype != torch.uint8:
+                raise ValueError("workspace must be a uint8 tensor")
+            rc = lib.draco_gguf_gemv_residual_ws(
+                int(ggml_type), qweight.data_ptr(), qweight.numel(), x.data_ptr(), _x_dtype(x), resid.data_ptr(),
+                rb, m, n, k, workspace.data_ptr(), workspace.numel(), _stream(x),
+            )
     _native.check(rc, "gguf_gemv_residual")
+
+
+def gemv_residual_workspace_bytes(ggml_type: int, m: int, n: int, k: int) -> int:
+    """Bytes of split-K workspace gguf_gemv_residual uses for this launch (0: none)."""
+    return int(_native.load().draco_gguf_gemv_residual_workspace_size(int(ggml_type), int(m), int(n), int(k)))
 
 
 def _norm_args(x: torch.Tensor, norm_weight: torch.Tensor, x_norm: torch.Tensor, k: int) -> int:

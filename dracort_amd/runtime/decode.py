@@ -40,6 +40,7 @@ from dracort_amd.kernels.gguf import (
     gguf_gemv_multi,
     gguf_gemv_multi_rmsnorm,
     gguf_gemv_residual,
+    gemv_residual_workspace_bytes,
     gguf_gemv_swiglu,
     gguf_gemv_swiglu_rmsnorm,
 )
@@ -228,6 +229,11 @@ class DecodeStep:
         self.s = torch.empty((m, s.inter), **b16)
         self.logits = torch.empty((m, s.vocab), **f32)
         self.graph: Optional[torch.cuda.CUDAGraph] = None
+        # split-K room of the residual projections (the down projection at
+        # several tokens); one buffer, the launches run one after another
+        ws_bytes = max([gemv_residual_workspace_bytes(w.ggml_type, m, w.shape[0], w.shape[1])
+                        for layer in ls.layers for w in (layer["o"], layer["down"])] + [0])
+        self.gemv_ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
         if attention is not None:
             a = attention
             if a.n_heads * a.head_dim != s.hidden or a.n_kv_heads * a.head_dim != s.kv_dim:
@@ -288,10 +294,10 @@ class DecodeStep:
             else:
                 for w, out in ((q, self.q), (k, self.k), (v, self.v)):
                     gguf_gemv_multi(self.h_bf16, [(w.data, w.shape[0])], w.ggml_type, s.hidden, [None], [out])
-            gguf_gemv_residual(self.q, o.data, o.ggml_type, o.shape, self.h, self.h_bf16)
+            gguf_gemv_residual(self.q, o.data, o.ggml_type, o.shape, self.h, self.h_bf16, workspace=self.gemv_ws)
             g, u, d = layer["gate"], layer["up"], layer["down"]
             gguf_gemv_swiglu(self.h_bf16, g.data, u.data, g.ggml_type, g.shape, out_bf16=self.s)
-            gguf_gemv_residual(self.s, d.data, d.ggml_type, d.shape, self.h, self.h_bf16)
+            gguf_gemv_residual(self.s, d.data, d.ggml_type, d.shape, self.h, self.h_bf16, workspace=self.gemv_ws)
         w = self.ls.lm_head
         gguf_gemv(self.h_bf16, w.data, w.ggml_type, w.shape, out=self.logits)
         return self.logits
@@ -320,11 +326,11 @@ class DecodeStep:
                     gguf_gemv_multi(self.xn, [(w.data, w.shape[0])], w.ggml_type, s.hidden, [out])
             decode_attention(self.qf, self.kf, self.vf, self.k_cache[li], self.v_cache[li], self.positions,
                              a.n_heads, a.n_kv_heads, rope=self.rope, out=self.att, workspace=self.ws)
-            gguf_gemv_residual(self.att, o.data, o.ggml_type, o.shape, self.h)
+            gguf_gemv_residual(self.att, o.data, o.ggml_type, o.shape, self.h, workspace=self.gemv_ws)
             g, u, d = layer["gate"], layer["up"], layer["down"]
             gguf_gemv_swiglu_rmsnorm(self.h, norms["ffn"], a.rms_eps, self.xn, g.data, u.data, g.ggml_type, g.shape,
                                      out_bf16=self.s)
-            gguf_gemv_residual(self.s, d.data, d.ggml_type, d.shape, self.h)
+            gguf_gemv_residual(self.s, d.data, d.ggml_type, d.shape, self.h, workspace=self.gemv_ws)
         w = self.ls.lm_head
         gguf_gemv_multi_rmsnorm(self.h, self.ls.output_norm, a.rms_eps, self.xn, [(w.data, w.shape[0])],
                                 w.ggml_type, s.hidden, [self.logits])

@@ -139,6 +139,21 @@ int draco_gguf_gemv_residual(int ggml_type, const void* w, size_t w_bytes, const
                              void* resid_bf16, int64_t m, int64_t n, int64_t k, void* stream);
 
 /*
+ * draco_gguf_gemv_residual with a workspace (device memory, 256-byte
+ * aligned): launches with few 16-row tiles and long rows (K > 4096, e.g. the
+ * down projection at 8..16 tokens) then split K over several workgroups per
+ * tile, store the partial sums to the workspace and add them in a fixed
+ * order in a second launch (the result does not depend on scheduling).  The
+ * bytes needed are draco_gguf_gemv_residual_workspace_size(type, m, n, k) (0:
+ * this launch is not split; a smaller workspace, or NULL, runs unsplit).
+ * Same reference call sites as draco_gguf_gemv_residual.
+ */
+size_t draco_gguf_gemv_residual_workspace_size(int ggml_type, int64_t m, int64_t n, int64_t k);
+int draco_gguf_gemv_residual_ws(int ggml_type, const void* w, size_t w_bytes, const void* x, int x_dtype,
+                                float* resid, void* resid_bf16, int64_t m, int64_t n, int64_t k, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+/*
  * Workspace bytes draco_gguf_gemm / draco_gguf_linear use for m token rows of
  * length k with this weight type (0 when the type's GEMM needs none).  Q4_K
  * requires m * k * 2 + 3 * m * (k / 32) * 2 + m * 4 bytes (rounded up to 256

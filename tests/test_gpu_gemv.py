@@ -145,3 +145,38 @@ def test_gemv_k_windows(qtype, m):
     got = resid.cpu().numpy()
     check_close(got, r0.astype(np.float64) + ref, f"windows residual {NAMES[qtype]} m={m}")
     assert np.array_equal(rb.float().cpu().numpy(), _bf16_round(got))
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K, Q4_0])
+@pytest.mark.parametrize("m,xdtype", [(16, torch.bfloat16), (8, torch.bfloat16), (12, torch.float32)])
+def test_gemv_residual_split_k(qtype, m, xdtype):
+    """Long rows (K = 14336) at 8..16 activation rows with a workspace: K is
+    split over several workgroups per 16-row tile and the partial sums are
+    added in split order by a second launch -- the same result on every call,
+    within the bar of the oracle like the unsplit launch (no workspace, or a
+    workspace one byte short)."""
+    from dracort_amd.kernels import gemv_residual_workspace_bytes, gguf_gemv_residual
+
+    n, k = 512, 14336
+    need = gemv_residual_workspace_bytes(qtype, m, n, k)
+    assert need == 7 * m * n * 4  # 56 chunks of 256 in 7 splits of 8
+    assert gemv_residual_workspace_bytes(qtype, 4, n, k) == 0  # below 8 rows: no split
+    blocks, w = quantized(qtype, n, k, 120 + m)
+    q = torch.from_numpy(blocks).cuda()
+    x = activations(m, k, 120 + m, xdtype).cuda()
+    ref = matmul_ref.linear_ref(x.cpu().float().numpy(), w)
+    r0 = np.random.default_rng(125 + m).standard_normal((m, n), dtype=np.float32)
+    print(f"split-K residual {NAMES[qtype]} m={m} {xdtype}", flush=True)
+    outs = []
+    for ws in (torch.empty(need, dtype=torch.uint8, device="cuda"),
+               torch.empty(need, dtype=torch.uint8, device="cuda"),
+               torch.empty(need - 1, dtype=torch.uint8, device="cuda"),
+               None):
+        resid = torch.from_numpy(r0.copy()).cuda()
+        rb = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        gguf_gemv_residual(x, q, qtype, (n, k), resid, rb, workspace=ws)
+        got = resid.cpu().numpy()
+        check_close(got, r0.astype(np.float64) + ref, f"split residual {NAMES[qtype]} m={m}")
+        assert np.array_equal(rb.float().cpu().numpy(), _bf16_round(got))
+        outs.append(got)
+    assert np.array_equal(outs[0], outs[1])

@@ -32,6 +32,7 @@
 
 #include "gemv_mfl.h"
 #include "gemv_stream.h"
+#include "gemv_x1b.h"
 
 namespace draco {
 
@@ -730,6 +731,11 @@ static int gemv_dispatch_mode(int qtype, bool d_last, const StreamJob& job, bool
     const int bpc = (MODE == kSwiGLU || MODE == kResid) ? 2 : job.rows >= 8192 ? 4 : 3;
     if (qtype == kQ4_K) return launch_x1p<kQ4_K, false, MODE, 1>(job, bpc, s);
     return d_last ? launch_x1p<kQ6_K, true, MODE, 1>(job, bpc, s) : launch_x1p<kQ6_K, false, MODE, 1>(job, bpc, s);
+  }
+  // one token, Q8_0 / Q4_0, rows of at most 4096: the block-format
+  // single-token kernel (activations in registers, gemv_x1b.h)
+  if constexpr (MODE != kSwiGLU) {
+    if (x1b_ok(qtype, job)) return x1b_dispatch<MODE>(qtype, job, xbf16, s);
   }
   // activation rows too long for the LDS image: the streaming kernel over K
   // windows -- bf16 rows below 8, float32 rows up to 4, and 5..8 float32

@@ -180,3 +180,42 @@ def test_gemv_residual_split_k(qtype, m, xdtype):
         assert np.array_equal(rb.float().cpu().numpy(), _bf16_round(got))
         outs.append(got)
     assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("qtype", [Q8_0, Q4_0])
+@pytest.mark.parametrize("xdtype", [torch.float32, torch.bfloat16])
+def test_gemv_single_token_block_formats(qtype, xdtype):
+    """One token over Q8_0 / Q4_0 rows of K <= 4096 (the block-format
+    single-token kernel: activations in registers, lanes past K idle): ragged
+    row counts, short rows, the bias, a three-matrix launch with bf16 copies,
+    and the residual epilogue."""
+    from dracort_amd.kernels import gguf_gemv_multi, gguf_gemv_residual
+
+    for n, k in ((1000, 4096), (64, 256), (3000, 2048), (17, 4096)):
+        print(f"single token {NAMES[qtype]} [{n},{k}] {xdtype}", flush=True)
+        y, ref = _run(qtype, n, k, 1, xdtype, seed=n + k, bias=(n == 1000))
+        check_close(y, ref, f"x1b {NAMES[qtype]} [{n},{k}] {xdtype}")
+
+    k = 1024
+    ns = (512, 128, 128)
+    x = activations(1, k, 7, xdtype)
+    qs, refs, outs, outs_b = [], [], [], []
+    for i, n in enumerate(ns):
+        blocks, w = quantized(qtype, n, k, 40 + i)
+        qs.append((torch.from_numpy(blocks).cuda(), n))
+        refs.append(matmul_ref.linear_ref(x.float().numpy(), w))
+        outs.append(torch.full((1, n), float("nan"), device="cuda"))
+        outs_b.append(torch.empty((1, n), device="cuda", dtype=torch.bfloat16))
+    gguf_gemv_multi(x.cuda(), qs, qtype, k, outs, outs_b)
+    for i in range(3):
+        got = outs[i].cpu().numpy()
+        check_close(got, refs[i], f"x1b multi {NAMES[qtype]} matrix {i}")
+        assert np.array_equal(outs_b[i].float().cpu().numpy(), _bf16_round(got))
+
+    r0 = np.random.default_rng(9).standard_normal((1, 512), dtype=np.float32)
+    resid = torch.from_numpy(r0.copy()).cuda()
+    rb = torch.empty((1, 512), device="cuda", dtype=torch.bfloat16)
+    gguf_gemv_residual(x.cuda(), qs[0][0], qtype, (512, k), resid, rb)
+    got = resid.cpu().numpy()
+    check_close(got, r0.astype(np.float64) + refs[0], f"x1b residual {NAMES[qtype]}")
+    assert np.array_equal(rb.float().cpu().numpy(), _bf16_round(got))

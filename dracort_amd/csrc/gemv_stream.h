@@ -67,6 +67,18 @@ struct StreamJob {
   int split_chunks;
 };
 
+// Element i (0..3) of four values by a chain of selects: indexing an array of
+// the kernel argument with a run-time index makes the compiler copy the
+// argument to scratch memory and load from there.
+template <class T>
+__device__ __forceinline__ T pick4(int i, T a, T b, T c, T d) {
+  T v = a;
+  v = i >= 1 ? b : v;
+  v = i >= 2 ? c : v;
+  v = i >= 3 ? d : v;
+  return v;
+}
+
 // Row r of this launch -> (matrix, row within it); rows of the matrices of a
 // kPlain launch are concatenated.
 __device__ __forceinline__ void row_of(const StreamJob& j, int r, int& mat, int& lrow) {
@@ -144,7 +156,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(StreamJob job, int row
         }
       }
     }
-    base = job.w[NR == 2 ? r : mat];
+    base = pick4(NR == 2 ? r : mat, job.w[0], job.w[1], job.w[2], job.w[3]);
     off = (int64_t)lrow * job.row_bytes;
   };
 
@@ -251,7 +263,8 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(StreamJob job, int row
   }
   if (!active) return;
   for (int s0 = 0; s0 < steps; s0 += NB) {
-#pragma unroll
+    // (fully unrolled: a run-time index into buf would put buf in scratch)
+#pragma clang loop unroll(full)
     for (int b = 0; b < NB; ++b) {
       load_step(buf[(b + kPrefetch) % NB]);
       compute_step(buf[b]);
@@ -276,7 +289,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(StreamJob job, int row
         }
       }
     }
-    const int n = job.n[mat];
+    const int n = pick4(mat, job.n[0], job.n[1], job.n[2], job.n[3]);
     const size_t o = (size_t)mi * n + lrow;
     if constexpr (MODE == kResid) {
       const float out = job.resid[o] + v;
@@ -284,8 +297,10 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(StreamJob job, int row
       if (job.resid_bf16) job.resid_bf16[o] = f32_to_bf16_rne(out);
     } else {
       const float out = v + ((MODE == kPlain && job.bias) ? job.bias[lrow] : 0.f);
-      if (job.y[mat]) job.y[mat][o] = out;
-      if (job.yb[mat]) job.yb[mat][o] = f32_to_bf16_rne(out);
+      float* const yp = pick4(mat, job.y[0], job.y[1], job.y[2], job.y[3]);
+      uint16_t* const ybp = pick4(mat, job.yb[0], job.yb[1], job.yb[2], job.yb[3]);
+      if (yp) yp[o] = out;
+      if (ybp) ybp[o] = f32_to_bf16_rne(out);
     }
   }
 }

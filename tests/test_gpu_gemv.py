@@ -115,11 +115,12 @@ def _bf16_round(a: np.ndarray) -> np.ndarray:
 @pytest.mark.parametrize("m", [2, 4, 8])
 def test_gemv_k_windows(qtype, m):
     """Float32 activation rows longer than the LDS activation image (m x k
-    floats > 64 KB): the launch runs as K windows of whole 2048-column steps --
-    bias added by the first window, later windows through the residual
-    epilogue, the bf16 copy written by the last.  Eight rows are windowed only
-    when two windows cover K; Q6_K (like Q2_K / Q3_K) is not windowed and
-    checks the same entry points on its unwindowed path."""
+    floats > 64 KB): the K-quant launches run as K windows of whole
+    2048-column steps -- bias added by the first window, later windows through
+    the residual epilogue, the bf16 copy written by the last.  Eight rows are
+    windowed only when two windows cover K; Q6_K (like Q2_K / Q3_K) is not
+    windowed, and Q4_0 / Q8_0 run on the float32 matrix-core kernel: both
+    check the same entry points on their own paths."""
     from dracort_amd.kernels import gguf_gemv_multi, gguf_gemv_residual
 
     n, k = 1000, (14336 if m <= 4 else 4096)
@@ -219,3 +220,55 @@ def test_gemv_single_token_block_formats(qtype, xdtype):
     got = resid.cpu().numpy()
     check_close(got, r0.astype(np.float64) + refs[0], f"x1b residual {NAMES[qtype]}")
     assert np.array_equal(rb.float().cpu().numpy(), _bf16_round(got))
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_gemv_float32_matrix_core(qtype):
+    """Float32 activations at 2..8 rows over Q4_0 / Q8_0 (the 4 x 4 x 1
+    float32 MFMA kernel: one 256-element K range per item, the wave's partial
+    tiles added in LDS): every row count on short and ragged rows (K ranges
+    cut inside, row counts off the 16-row tile), one to four tiles per
+    workgroup, uneven K ranges per wave (K = 14336), a three-matrix launch with
+    bf16 copies, the residual epilogue, and the same bits on a second call."""
+    from dracort_amd.kernels import gguf_gemv_multi, gguf_gemv_residual
+
+    for n, k in ((16, 64), (33, 320), (130, 1088)):
+        for m in range(2, 9):
+            print(f"mf32 {NAMES[qtype]} [{n},{k}] m={m}", flush=True)
+            y, ref = _run(qtype, n, k, m, torch.float32, seed=n + k + m, bias=(m == 5))
+            check_close(y, ref, f"mf32 {NAMES[qtype]} [{n},{k}] m={m}")
+    for n, k, m in ((4100, 4096, 3), (4100, 4096, 8), (16000, 1024, 5), (9000, 512, 2), (1000, 14336, 7)):
+        print(f"mf32 {NAMES[qtype]} [{n},{k}] m={m}", flush=True)
+        y, ref = _run(qtype, n, k, m, torch.float32, seed=n + m)
+        check_close(y, ref, f"mf32 {NAMES[qtype]} [{n},{k}] m={m}")
+
+    k, m = 1024, 6
+    ns = (512, 128, 128)
+    mats = [quantized(qtype, n, k, 300 + i) for i, n in enumerate(ns)]
+    x = activations(m, k, 310, torch.float32)
+    ys = [torch.full((m, n), float("nan"), device="cuda") for n in ns]
+    ybs = [torch.empty((m, n), device="cuda", dtype=torch.bfloat16) for n in ns]
+    print(f"mf32 multi {NAMES[qtype]}", flush=True)
+    gguf_gemv_multi(x.cuda(), [(torch.from_numpy(b).cuda(), n) for (b, _), n in zip(mats, ns)], qtype, k, ys, ybs)
+    for i, ((_, w), n) in enumerate(zip(mats, ns)):
+        got = ys[i].cpu().numpy()
+        check_close(got, matmul_ref.linear_ref(x.numpy(), w), f"mf32 multi {i}")
+        assert np.array_equal(ybs[i].float().cpu().numpy(), _bf16_round(got))
+
+    for n, k, m in ((4096, 14336, 7), (500, 4096, 3)):
+        blocks, w = quantized(qtype, n, k, 320 + m)
+        q = torch.from_numpy(blocks).cuda()
+        x = activations(m, k, 330 + m, torch.float32).cuda()
+        ref = matmul_ref.linear_ref(x.cpu().numpy(), w)
+        r0 = np.random.default_rng(340 + m).standard_normal((m, n), dtype=np.float32)
+        print(f"mf32 residual {NAMES[qtype]} [{n},{k}] m={m}", flush=True)
+        outs = []
+        for _ in range(2):
+            resid = torch.from_numpy(r0.copy()).cuda()
+            rb = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+            gguf_gemv_residual(x, q, qtype, (n, k), resid, rb)
+            got = resid.cpu().numpy()
+            check_close(got, r0.astype(np.float64) + ref, f"mf32 residual {NAMES[qtype]} [{n},{k}] m={m}")
+            assert np.array_equal(rb.float().cpu().numpy(), _bf16_round(got))
+            outs.append(got)
+        assert np.array_equal(outs[0], outs[1])

@@ -257,8 +257,9 @@ def rotation(make, nbytes, min_total=1 << 30):
     return [first] + [torch.empty_like(first).copy_(first) for _ in range(n - 1)]
 
 
-def suite(reps: int):
-    """The other configurations of the path, one JSON line each (stdout)."""
+def suite(reps: int, gemv_only: bool = False):
+    """The other configurations of the path, one JSON line each (stdout);
+    ``gemv_only``: configurations 1 and 2 only (kernel traces)."""
     import torch
 
     from dracort_amd.format.gguf import tensor_bytes
@@ -288,6 +289,8 @@ def suite(reps: int):
     for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
         for m in (1, 4, 8):
             lines.append(gemv_line(2, 2, n, k, m, torch.float32))
+    if gemv_only:
+        return lines
     # 3 (single kernels): Q4_K / Q6_K GEMVs at M = 1 and 16, bf16 activations
     for t, n, k in ((12, 14336, 4096), (12, 4096, 4096), (14, 4096, 14336), (14, 128256, 4096)):
         for m in (1, 16):
@@ -656,6 +659,7 @@ def main() -> int:
     ap.add_argument("--full-context", type=int, default=1024,
                     help="also time the full decode step (norms + attention) at this context (0: skip)")
     ap.add_argument("--suite", action="store_true", help="measure configurations 1, 2, 4, 5 (one JSON line each)")
+    ap.add_argument("--gemv-probe", action="store_true", help="configurations 1 and 2 only (kernel traces)")
     ap.add_argument("--types", action="store_true", help="decode GEMV of every GGUF block type (one JSON line each)")
     ap.add_argument("--traffic-probe", action="store_true", help="run only the roofline rotation + a 256 MB copy")
     ap.add_argument("--mfma-probe", action="store_true", help="run only the configuration-4 GEMMs (counter runs)")
@@ -682,8 +686,8 @@ def main() -> int:
         log("no GPU visible")
         return 1
     torch.cuda.set_device(0)
-    if args.suite:
-        for line in suite(args.roofline_reps):
+    if args.suite or args.gemv_probe:
+        for line in suite(args.roofline_reps, gemv_only=args.gemv_probe):
             print(json.dumps(line), flush=True)
         return 0
     if args.types:

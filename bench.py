@@ -480,6 +480,87 @@ def stream_probe(reps: int):
     return lines
 
 
+def chain_probe(reps: int):
+    """Read-only chains with the decode step's launch sizes (32 x [q/k/v, o,
+    gate + up, down] + lm_head, 4 841 250 816 B, one buffer beyond the
+    Infinity Cache): one launch per phase, with and without a page-translation
+    warm-up of the next phase (one 16-byte word per 64 KB touched in each
+    launch's last step), against one persistent cooperative launch over all
+    phases with no synchronisation (the bound) and with a grid-wide barrier
+    between phases (relaxed, or with release / acquire fences).  HIP events
+    around `reps` back-to-back chains.  One JSON line per variant."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(PROBE_LIB)
+    lib.draco_probe_chain_launches.restype = ctypes.c_int
+    lib.draco_probe_chain_launches.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    lib.draco_probe_chain_persistent.restype = ctypes.c_int
+    lib.draco_probe_chain_persistent.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                                 ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+    sizes = [14155776, 9437184, 66060288, 48168960] * 32 + [430940160]
+    offs, tot = [], 0
+    for nb in sizes:
+        offs += [tot // 16, nb // 16]
+        tot += nb
+    buf = torch.empty(tot, dtype=torch.uint8, device="cuda").random_(0, 255)
+    ph_host = (ctypes.c_int64 * len(offs))(*offs)
+    ph_dev = torch.tensor(offs, dtype=torch.int64, device="cuda")
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    stream = torch.cuda.current_stream()
+    n = len(sizes)
+
+    def timed(run):
+        run()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            run()
+        b.record(stream)
+        b.synchronize()
+        return a.elapsed_time(b) / reps
+
+    lines = []
+
+    def emit(variant, ms, **kw):
+        line = {"probe": "launch_chain", "variant": variant, "phases": n, "bytes": tot,
+                "us_per_chain": round(ms * 1e3, 1), "GB_s": round(tot / (ms * 1e-3) / 1e9, 1), **kw}
+        log(json.dumps(line))
+        lines.append(line)
+
+    for stride_kb in (0, 64, 2048):
+        def run(stride_kb=stride_kb):
+            rc = lib.draco_probe_chain_launches(buf.data_ptr(), ph_host, n, 8 * cus, stride_kb * 1024 // 16,
+                                                sink.data_ptr(), stream.cuda_stream)
+            assert rc == 0, rc
+        emit("one launch per phase" + (f", next-phase pages touched every {stride_kb} KB" if stride_kb else ""),
+             timed(run), workgroups=8 * cus)
+    names = {0: "persistent, no synchronisation", 1: "persistent, relaxed grid barrier per phase",
+             2: "persistent, release/acquire grid barrier per phase"}
+    for mode in (0, 1, 2):
+        counters = [torch.zeros(32 * 32, dtype=torch.int32, device="cuda") for _ in range(reps + 1)]
+        it = iter(counters)
+
+        def run(mode=mode):
+            rc = lib.draco_probe_chain_persistent(buf.data_ptr(), ph_dev.data_ptr(), n, 2 * cus, mode,
+                                                  next(it).data_ptr(), err.data_ptr(), sink.data_ptr(),
+                                                  stream.cuda_stream)
+            assert rc == 0, rc
+        ms = timed(run)
+        torch.cuda.synchronize()
+        emit(names[mode], ms, workgroups=2 * cus, timed_out_waits=int(err.item()))
+    base = lines[3]["us_per_chain"]
+    for line in lines[4:]:
+        line["us_per_barrier"] = round((line["us_per_chain"] - base) / (n - 1), 3)
+    return lines
+
+
 def _timed_cpu(fn, budget_s):
     """Mean seconds per call of fn, repeated until budget_s has passed (at least twice, after one warm call)."""
     fn()
@@ -664,6 +745,8 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true", help="run only the roofline rotation + a 256 MB copy")
     ap.add_argument("--mfma-probe", action="store_true", help="run only the configuration-4 GEMMs (counter runs)")
     ap.add_argument("--moe-probe", action="store_true", help="run only the configuration-5 MoE FFN (kernel traces)")
+    ap.add_argument("--chain-probe", action="store_true",
+                    help="read-only chains of the step's launch sizes: launches vs one persistent kernel with barriers")
     ap.add_argument("--stream-probe", action="store_true",
                     help="time a read-only kernel on each decode-launch size (the single-launch ceiling)")
     ap.add_argument("--no-configs", action="store_true",
@@ -702,6 +785,10 @@ def main() -> int:
         return 0
     if args.moe_probe:
         moe_probe(3)
+        return 0
+    if args.chain_probe:
+        for line in chain_probe(10):
+            print(json.dumps(line), flush=True)
         return 0
     if args.stream_probe:
         for line in stream_probe(args.roofline_reps):

@@ -259,8 +259,13 @@ __device__ __forceinline__ void x1_fetch_x_rmsnorm(const float* __restrict__ h, 
 // waited on it there -- eight serialized loads in the 14336-wide down
 // projection (Q6_K 4096 x 14336: 14.8 us, 14.1 with the loads issued together;
 // Q4_K 10.8 -> 10.5 us).
+//
+// The slots and group sums of the units past the row end in the last step are
+// zeroed, so every lane reads its step's activations without a mask (its
+// weights there are the last unit's again, which meet zeros).
 template <int QT, int XC>
 __device__ __forceinline__ void x1_stage_regs(uint4* lds, const uint4 (&xr)[XC], int k) {
+  constexpr int G = X1Fmt<QT>::G;
   const int chunks = k >> 3;
   const int pad = (int)(x1_lds_bytes(QT, k) / 16);
 #pragma unroll
@@ -269,6 +274,14 @@ __device__ __forceinline__ void x1_stage_regs(uint4* lds, const uint4 (&xr)[XC],
     const int cc = min(c, chunks - 1);
     const int slot = (cc >> 9) * 512 + x1_slot_of_chunk<QT>(cc & 511);
     lds[c < chunks ? slot : pad + (int)threadIdx.x] = xr[j];
+  }
+  const int units = k >> 6, steps = (units + 63) >> 6;
+  const int l0 = units - 64 * (steps - 1);  // first dead lane of the last step
+  float* sums = reinterpret_cast<float*>(lds + steps * 512);
+  for (int i = threadIdx.x; i < (64 - l0) * 8; i += blockDim.x) {
+    const int l = l0 + (i >> 3), j = i & 7;
+    lds[(steps - 1) * 512 + j * 64 + l] = uint4{0u, 0u, 0u, 0u};
+    if (j < G) sums[((steps - 1) * G + j) * 64 + l] = 0.f;
   }
   __syncthreads();
   x1_stage_sums<QT>(lds, k);
@@ -607,46 +620,49 @@ template <int QT, bool DL, int MODE, int S, int PF>
 __global__ __launch_bounds__(256) void gemv_x1s_kernel(StreamJob job) {
   static_assert(MODE != kSwiGLU, "one matrix per row");
   constexpr int NB = PF + 1;  // item ring: the current item and PF in flight
+  // rows per unrolled iteration: enough that every item's ring slot and step
+  // are compile-time constants (the unit offsets of each step are then per-lane
+  // constants of the launch)
+  constexpr int RU = S % NB == 0 ? 1 : NB;
+  constexpr int U = RU * S;
   extern __shared__ uint4 x1_smem[];
   const int lane = threadIdx.x & 63;
   const X1Rows<MODE> rows(job);
   const int nrow = rows.nrow;
   const int k = job.k;
   const int units = k >> 6;
+  // the lane's unit of each step (lanes past the row end re-read the last
+  // unit; their activations and sums are zero in the image)
+  int ul[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) ul[s] = min(lane + 64 * s, units - 1);
 
   // 1. activations (2 S 16-byte chunks per thread), then the first item
   uint4 xr[2 * S];
   x1_fetch_x<2 * S>(job.x, k, xr);
   X1Raw<QT> buf[NB];
 #pragma unroll
-  for (int p = 0; p < PF; ++p) {
-    const int ip = p / S, sp = p - ip * S;
-    const int up = lane + 64 * sp;
-    buf[p] = x1_load<QT, DL>(rows.buf(job, ip, 0), up < units ? up : units - 1);
-  }
+  for (int p = 0; p < PF; ++p) buf[p] = x1_load<QT, DL>(rows.buf(job, p / S, 0), ul[p % S]);
 
   // 2. the LDS image and group sums
   x1_stage_regs<QT, 2 * S>(x1_smem, xr, k);
   if (nrow == 0) return;
   const X1Lane lc = x1_lane<QT>(lane);
 
-  // 3. items t = (row t / S, step t % S), NB per iteration so the ring
-  // index is static
-  const int total = nrow * S;
+  // 3. items (row i, step s), U per iteration
   float res = 0.f, acc = 0.f;
-  for (int t0 = 0; t0 < total; t0 += NB) {
+  for (int i0 = 0; i0 < nrow; i0 += RU) {
 #pragma unroll
-    for (int p = 0; p < NB; ++p) {
-      const int t = t0 + p;
-      const int in = (t + PF) / S, sn = (t + PF) - in * S;
-      const int un = lane + 64 * sn;
-      buf[(p + PF) % NB] = x1_load<QT, DL>(rows.buf(job, in, 0), un < units ? un : units - 1);
+    for (int p = 0; p < U; ++p) {
+      const int i = i0 + p / S;
+      const int s = p % S;
+      const int pn = p + PF;
+      buf[pn % NB] = x1_load<QT, DL>(rows.buf(job, i0 + pn / S, 0), ul[pn % S]);
       __builtin_amdgcn_sched_barrier(0);  // keep the load ahead of the math
-      if (t < total) {
-        const int i = t / S, s = t - i * S;
+      if (i < nrow) {
         X1Act xa;
-        x1_read_lds<QT>(x1_smem, k, s, lane, lane + 64 * s < units, xa);
-        acc += x1_unit_dot<QT>(buf[p], lc, xa);
+        x1_read_lds<QT>(x1_smem, k, s, lane, true, xa);
+        acc += x1_unit_dot<QT>(buf[p % NB], lc, xa);
         if (s == S - 1) {
           const float v = wave_sum_dpp(acc);
           acc = 0.f;

@@ -279,43 +279,66 @@ __global__ __launch_bounds__(256) void moe_up_mfma_kernel(ExpertPtrs wg, ExpertP
   }
 }
 
-// Persistent form of the up projection for Q4_K experts with hidden <= 4096:
-// grid (workgroups per expert, experts); for each 16-token tile of its
-// expert a workgroup loads the gathered activations into registers once
-// (eight waves split the hidden dimension) and streams its share of the
-// gate/up row tiles against them through LDS (mfl_stream_q4k).
+// Persistent form of the up projection for Q4_K experts with hidden <= 4096,
+// one 512-thread workgroup per CU.  The work -- every 16-token tile of every
+// expert (expert e has ceil(counts[e] / 16) of them, known only on the
+// device) times the I / 16 row tiles of its gate / up matrices -- is cut
+// into gridDim.x runs of equally many row tiles in (expert, token tile, row
+// tile) order, one run per workgroup, so every CU streams the same number of
+// tiles whatever the routing (a grid of one workgroup per (expert, token
+// tile) slice left the slices of crowded experts to a second round).  A run
+// spans few token tiles; for each the workgroup loads the 16 gathered
+// tokens' activations into registers (eight waves split the hidden
+// dimension) and streams its row tiles through LDS (mfl_stream_q4k).
 __global__ __launch_bounds__(512) void moe_up_mfp_kernel(ExpertPtrs wg, ExpertPtrs wu,
-                                                         const uint16_t* __restrict__ x, int H, int I, MoeWs ws) {
+                                                         const uint16_t* __restrict__ x, int H, int I, int E,
+                                                         MoeWs ws) {
   constexpr int W = 8;
   __shared__ __attribute__((aligned(16))) uint8_t wl[2 * mfl_tile_lds(kMflMaxRowBytes)];
   __shared__ mf_f32x4 part[W][2][64];
-  const int e = blockIdx.y;
-  const int cnt = ws.counts[e];
-  if (cnt == 0) return;
-  const int off = ws.offsets[e];
+  __shared__ int tb[kMaxExperts + 1];  // token tiles of the experts before e
   const int lane = threadIdx.x & 63;
   const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int q = lane >> 4, nl = lane & 15;
-  const int chunks = H >> 8;
-  const int ntiles = I >> 4;
-  const int my_tiles = ntiles > (int)blockIdx.x ? (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int e = 0; e < E; ++e) {
+      tb[e] = acc;
+      acc += (ws.counts[e] + 15) >> 4;
+    }
+    tb[E] = acc;
+  }
+  __syncthreads();
+  const int chunks = H >> 8, rt = I >> 4;
+  const int64_t work = (int64_t)tb[E] * rt;
+  const int64_t lo = work * (int64_t)blockIdx.x / (int64_t)gridDim.x;
+  const int64_t hi = work * ((int64_t)blockIdx.x + 1) / (int64_t)gridDim.x;
   const int row_bytes = (H / 256) * 144;
-  const uint8_t* const gp = wg.p[e];
-  const uint8_t* const upp = wu.p[e];
+  const uint32_t mat_bytes = (uint32_t)I * (uint32_t)row_bytes;
   uint16_t* const hp = ws.hp;
   const size_t plane = ws.hp_plane;
-  const uint32_t mat_bytes = (uint32_t)I * (uint32_t)row_bytes;
-  for (int t0 = 16 * (int)blockIdx.z; t0 < cnt; t0 += 16 * (int)gridDim.z) {
-    const int mt = min(16, cnt - t0);
+  for (int64_t idx = lo; idx < hi;) {
+    // this segment: token tile `item` (expert e, tokens t0 ..), row tiles r0 .. r0 + nr
+    const int item = __builtin_amdgcn_readfirstlane((int)(idx / rt));
+    const int r0 = __builtin_amdgcn_readfirstlane((int)(idx - (int64_t)item * rt));
+    const int nr = __builtin_amdgcn_readfirstlane((int)min((int64_t)(rt - r0), hi - idx));
+    int e = 0;
+    while (tb[e + 1] <= item) ++e;  // item < tb[E]; experts without tokens are skipped
+    e = __builtin_amdgcn_readfirstlane(e);
+    const int t0 = 16 * (item - tb[e]);
+    const int off = ws.offsets[e];
+    const int mt = min(16, ws.counts[e] - t0);
     const int tok = ws.assign_tok[off + t0 + min(nl, mt - 1)];
+    const uint8_t* const gp = wg.p[e];
+    const uint8_t* const upp = wu.p[e];
     typename MfpTypes<kQ4_K>::X xr[16 / W];
     mfp_load_x<kQ4_K, W>(x + (size_t)tok * H, chunks, ks, q, xr);
     auto tile_base = [=](int i, int r) {
-      const int row = 16 * ((int)blockIdx.x + i * (int)gridDim.x);
+      const int row = 16 * (r0 + i);
       return MfRow{make_rsrc(r == 0 ? gp : upp, mat_bytes), row * row_bytes};
     };
     auto emit = [=](int i, const mf_f32x4 (&tot)[2]) {
-      const int col = 16 * ((int)blockIdx.x + i * (int)gridDim.x) + nl;
+      const int col = 16 * (r0 + i) + nl;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int m = 4 * q + v;  // D layout: lane l holds token rows 4 (l / 16) + v, weight row l % 16
@@ -329,7 +352,8 @@ __global__ __launch_bounds__(512) void moe_up_mfp_kernel(ExpertPtrs wg, ExpertPt
         }
       }
     };
-    mfl_stream_q4k<2, W>(xr, chunks, my_tiles, row_bytes, tile_base, emit, wl, part);
+    mfl_stream_q4k<2, W>(xr, chunks, nr, row_bytes, tile_base, emit, wl, part);
+    idx += nr;
   }
 }
 
@@ -421,10 +445,9 @@ static int launch_moe(const ExpertPtrs& wg, const ExpertPtrs& wu, const ExpertPt
       // not serialize its tiles
       const unsigned zt = (unsigned)std::min((T + 15) / 16, 8);
       if (QT == kQ4_K && xbf16 && H <= 4096) {
-        // one workgroup per CU, split evenly over the experts
-        const int per_expert = std::max(1, (device_cus() + E - 1) / E);
-        hipLaunchKernelGGL(moe_up_mfp_kernel, dim3((unsigned)per_expert, (unsigned)E, zt), dim3(512), 0, s, wg, wu,
-                           static_cast<const uint16_t*>(x), H, I, ws);
+        // one workgroup per CU, the routed work split evenly over them
+        hipLaunchKernelGGL(moe_up_mfp_kernel, dim3((unsigned)device_cus()), dim3(512), 0, s, wg, wu,
+                           static_cast<const uint16_t*>(x), H, I, E, ws);
       } else if (xbf16)
         hipLaunchKernelGGL((moe_up_mfma_kernel<QT, true>), dim3((unsigned)(I / 16), (unsigned)E, zt), dim3(256), 0, s,
                            wg, wu, x, H, I, ws);

@@ -24,6 +24,7 @@ Printed (one JSON line on stdout):
   configs    configurations 1, 2, 4 and 5 at full size on the GPU, each with
              the reference CPU path timed beside it (warm, cold, one thread)
   full_decode  the complete decode step (norms, RoPE, KV cache, attention)
+  batch16    the projection step and the full step for 16 sequences at once
 Modes: --stream-probe (read-only kernel at each launch size: the per-launch
 ceiling), --suite / --types / --traffic-probe / --mfma-probe / --moe-probe.
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
@@ -749,6 +750,7 @@ def main() -> int:
                     help="read-only chains of the step's launch sizes: launches vs one persistent kernel with barriers")
     ap.add_argument("--stream-probe", action="store_true",
                     help="time a read-only kernel on each decode-launch size (the single-launch ceiling)")
+    ap.add_argument("--no-batch16", action="store_true", help="skip the batch-16 decode steps of the default line")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip configurations 1, 2, 4, 5 (GPU and CPU) in the default run")
     args = ap.parse_args()
@@ -830,6 +832,30 @@ def main() -> int:
         full = full_decode(ls, args.batch, args.full_context, max(10, args.steps // 2), 2)
         log(f"full decode step: {full}")
 
+    # the same layer set decoded for 16 sequences at once (one token each):
+    # the projection step and the full step, reported beside the batch-1 value
+    batch16 = None
+    if args.batch == 1 and not args.no_batch16:
+        b16 = DecodeStep(ls, m=16)
+        b16.capture()
+        for _ in range(3):
+            b16.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n16 = max(10, args.steps // 2)
+        e0.record(stream)
+        for _ in range(n16):
+            b16.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms16 = e0.elapsed_time(e1) / n16
+        del b16
+        torch.cuda.empty_cache()
+        batch16 = {"batch": 16, "ms_per_step": round(ms16, 4), "tokens_per_s": round(16e3 / ms16, 2),
+                   "weight_GB_s": round(step_bytes / (ms16 * 1e-3) / 1e9, 1), "steps": n16,
+                   "full_decode": full_decode(ls, 16, args.full_context, n16, 2) if args.full_context > 0 else None}
+        log(f"batch-16 decode: {batch16}")
+
     roof = dominant_kernel_roofline(ls, args.roofline_reps)
     log(f"roofline: {roof}")
     dom = step_dominant_roofline(ls, args.roofline_reps)
@@ -876,6 +902,7 @@ def main() -> int:
         "tokens_per_s": round(args.batch * 1e3 / ms, 2),
         "pct_of_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "full_decode": full,
+        "batch16": batch16,
         "roofline": roof,
         "roofline_step_dominant": dom,
         "cpu_baseline": cpu,

@@ -49,12 +49,19 @@ __device__ __forceinline__ int g2_fresh(int v) {
 // Split K: with part != nullptr the grid holds `splits` workgroups per output
 // tile, split s taking super-blocks [s sbps, (s + 1) sbps) and storing its raw
 // sums to part[s][M][N]; gemm_split_reduce_kernel adds them in split order.
+// Tail split (tail_s > 1): the first tail_full tiles (whole weight-tile
+// columns) run whole, and the rest, the partial last round of a grid that
+// does not divide evenly over the CUs, in tail_s parts of K each (raw sums to
+// part[s][M][N - n_tail] for columns n_tail .. N - 1, added by the reduce
+// launch), so every CU finishes the launch with the same amount of work.
+// Each XCD gets tail_full / 8 whole tiles, then its share of the parts.
 template <int WM, int WN, int NS = 2>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* __restrict__ w, GemmQ4kWs ws,
                                                                  const float* __restrict__ bias,
                                                                  float* __restrict__ y, int M, int N, int K,
                                                                  int tiles_m, int tiles, int sbps,
-                                                                 float* __restrict__ part) {
+                                                                 float* __restrict__ part, int tail_full,
+                                                                 int tail_s) {
   constexpr int NT = WM * WN * 64;          // threads
   constexpr int BM = 64 * WM, BN = 64 * WN;  // workgroup tile
   constexpr int BK = 64, LDK = BK + 8;       // f16 per LDS row (144 B)
@@ -74,16 +81,30 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* 
   // tile share that XCD's L2)
   const int nb = gridDim.x;
   int bid = blockIdx.x;
-  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-  const int split = bid / tiles;
-  bid -= split * tiles;
+  int split;
+  if (tail_s > 1) {
+    // (the launch guarantees tail_full % 8 == 0 and nb % 8 == 0)
+    const int xcd = bid & 7, k8 = bid >> 3, full8 = tail_full >> 3;
+    if (k8 < full8) {
+      bid = xcd * full8 + k8;
+      split = -1;
+    } else {
+      const int h = xcd * ((nb - tail_full) >> 3) + (k8 - full8);
+      bid = tail_full + h / tail_s;
+      split = h - (h / tail_s) * tail_s;
+    }
+  } else {
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    split = bid / tiles;
+    bid -= split * tiles;
+  }
   const int tm = bid % tiles_m, tn = bid / tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WM, wn = wave / WM;
   const int sbs = K >> 8, groups = K >> 5;
-  const int sb0 = split * sbps, sb1 = min(sb0 + sbps, sbs), ks0 = 4 * sb0;
+  const int sb0 = split < 0 ? 0 : split * sbps, sb1 = split < 0 ? sbs : min(sb0 + sbps, sbs), ks0 = 4 * sb0;
   const uint32_t row_bytes = (uint32_t)sbs * 144u;
   const __amdgpu_buffer_rsrc_t wrs = make_rsrc(w, (uint32_t)N * row_bytes);
   // activations and sums through buffer resources: 32-bit offsets, and reads
@@ -315,12 +336,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* 
     for (int v = 0; v < 16; ++v) {
       const int m = m0 + wm * 64 + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
       if (m >= M) continue;
-      if (part) {
-        float* pr = part + ((size_t)split * M + m) * N;
+      if (part && split >= 0) {
+        // raw sums: columns nt .. N - 1 (all of them unless tail split)
+        const int nt = tail_s > 1 ? (tail_full / tiles_m) * 128 : 0;
+        float* pr = part + ((size_t)split * M + m) * (size_t)(N - nt);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int n = n0 + wn * 64 + 32 * j + fr;
-          if (n < N) pr[n] = acc[i][j][v];
+          if (n < N) pr[n - nt] = acc[i][j][v];
         }
         continue;
       }
@@ -333,20 +356,21 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_q4k2_kernel(const uint8_t* 
     }
 }
 
-// y[m, n] = (sum over s in order of part[s][m][n]) * 2^t_m + bias[n]: one
-// thread per output, fixed summation order (the result does not depend on
-// which split finished first).
+// y[m, n] = (sum over s in order of part[s][m][n - nt]) * 2^t_m + bias[n] for
+// the columns n >= nt that were split: one thread per output, fixed
+// summation order (the result does not depend on which split finished first).
 __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __restrict__ part, int splits, int M,
-                                                                int N, const float* __restrict__ rsc,
+                                                                int N, int nt, const float* __restrict__ rsc,
                                                                 const float* __restrict__ bias,
                                                                 float* __restrict__ y) {
-  const size_t total = (size_t)M * N;
+  const int ns = N - nt;
+  const size_t total = (size_t)M * ns;
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= total) return;
-  const int m = (int)(i / (size_t)N), n = (int)(i - (size_t)m * N);
+  const int m = (int)(i / (size_t)ns), n = nt + (int)(i - (size_t)m * ns);
   float acc = part[i];
   for (int s = 1; s < splits; ++s) acc += part[(size_t)s * total + i];
-  y[i] = acc * rsc[m] + (bias ? bias[n] : 0.f);
+  y[(size_t)m * N + n] = acc * rsc[m] + (bias ? bias[n] : 0.f);
 }
 
 // Split-K plan of the 256 x 128 tiling for an M x N x K problem: `splits`
@@ -357,9 +381,11 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
 // vs 209 us unsplit, 110 us in four splits; M = 64 of 4096 x 14336 in eight
 // splits 54 vs 190 us.
 struct GemmQ4k2Plan {
-  int splits = 0;  // 0: not this kernel; 1: no partial sums
+  int splits = 0;  // 0: not this kernel; 1: no partial sums (unless tail split)
   int sbps = 0;    // super-blocks per split
   size_t part_bytes = 0;
+  // tail split: tiles [0, tail_full) whole, the rest in tail_s parts
+  int tail_full = 0, tail_s = 0;
 };
 
 // Workspace bytes the split-K partial sums of an M-row problem may need
@@ -367,9 +393,10 @@ struct GemmQ4k2Plan {
 // times the splits stays within the CU count, so S x N <= 128 x CUs / tiles_m.
 // The bound is taken at 256 CUs (MI355X), independent of the device present:
 // on a device with more CUs the splits are capped by the space given.
+// (The tail split of a grid of whole rounds plus a partial one keeps within
+// the same bound: its parts times their columns' tiles stay within the CUs.)
 inline size_t gemm_q4k2_part_bound(int64_t m) {
   const int64_t tiles_m = (m + 255) / 256;
-  if (tiles_m > 4) return 0;  // M > 1024: enough tiles without splitting
   return (size_t)m * 128 * (size_t)(256 / tiles_m) * 4;
 }
 
@@ -381,6 +408,26 @@ inline GemmQ4k2Plan gemm_q4k2_plan(int m, int n, int k, size_t part_avail) {
   if (tiles * 4 >= cus * 3) {
     pl.splits = 1;
     pl.sbps = k / 256;
+    // whole rounds plus a partial one: the partial round's tiles in parts of
+    // K, so it takes a fraction of a round (14336 x 4096 at M = 2048: 896
+    // tiles = 3 rounds + 128 tiles in two parts each).  The split tiles must
+    // be whole weight-tile columns, and the whole tiles and the parts divide
+    // evenly over the 8 XCDs.
+    const int64_t tiles_m = (m + 255) / 256;
+    const int64_t full = (tiles / cus) * cus, rest = tiles - full;
+    const int sbs = k / 256;
+    if (full > 0 && rest > 0 && full % tiles_m == 0 && full % 8 == 0) {
+      int ts = (int)std::min<int64_t>(cus / rest, sbs / 2);
+      while (ts >= 2 && (rest * ts) % 8 != 0) --ts;
+      const int64_t nt = full / tiles_m * 128;
+      const size_t bytes = (size_t)ts * m * (size_t)(n - nt) * 4;
+      if (ts >= 2 && nt < n && bytes <= part_avail) {
+        pl.tail_full = (int)full;
+        pl.tail_s = ts;
+        pl.sbps = (sbs + ts - 1) / ts;
+        pl.part_bytes = bytes;
+      }
+    }
     return pl;
   }
   const int sbs = k / 256;
@@ -405,17 +452,20 @@ inline int launch_gemm_q4k2(const void* w, const void* x, const float* bias, flo
                             void* workspace, const GemmQ4k2Plan& plan, hipStream_t s) {
   GemmQ4kWs ws;
   const size_t base = gemm_q4k_ws_layout(m, k, static_cast<char*>(workspace), &ws);
-  float* part = plan.splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + base) : nullptr;
+  const bool tail = plan.tail_s > 1;
+  float* part = plan.splits > 1 || tail ? reinterpret_cast<float*>(static_cast<char*>(workspace) + base) : nullptr;
   hipLaunchKernelGGL(gemm_prep_kernel, dim3((unsigned)m), dim3(256), 0, s, static_cast<const uint16_t*>(x), m, k, ws);
   if (int rc = check_launch("gemm_prep")) return rc;
   const int tiles_n = (n + 127) / 128, tiles_m = (m + 255) / 256, tiles = tiles_m * tiles_n;
-  hipLaunchKernelGGL((gemm_q4k2_kernel<4, 2>), dim3((unsigned)(tiles * plan.splits)), dim3(512), 0, s,
-                     static_cast<const uint8_t*>(w), ws, bias, y, m, n, k, tiles_m, tiles, plan.sbps, part);
+  const int grid = tail ? plan.tail_full + (tiles - plan.tail_full) * plan.tail_s : tiles * plan.splits;
+  hipLaunchKernelGGL((gemm_q4k2_kernel<4, 2>), dim3((unsigned)grid), dim3(512), 0, s, static_cast<const uint8_t*>(w),
+                     ws, bias, y, m, n, k, tiles_m, tiles, plan.sbps, part, plan.tail_full, plan.tail_s);
   if (int rc = check_launch("gemm_q4k2")) return rc;
   if (!part) return 0;
-  const size_t total = (size_t)m * n;
+  const int nt = tail ? plan.tail_full / tiles_m * 128 : 0;
+  const size_t total = (size_t)m * (n - nt);
   hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part,
-                     plan.splits, m, n, ws.rsc, bias, y);
+                     tail ? plan.tail_s : plan.splits, m, n, nt, ws.rsc, bias, y);
   return check_launch("gemm_split_reduce");
 }
 

@@ -115,6 +115,35 @@ def test_gemm_q4k_split_k(n, k, m):
     check_close(y3.numpy(), ref, f"gemm Q4_K unsplit [{n},{k}] m={m}")
 
 
+def test_gemm_q4k_tail_split():
+    """A grid of whole rounds plus a partial one (2048 x 5120: 320 tiles of
+    256 x 128 on 256 CUs): the partial round's tiles run in parts of K whose
+    raw sums a second launch adds in split order for their columns only, the
+    rest of the tiles whole.  Deterministic from run to run and, like the
+    unsplit launch (workspace without the split room), within the bar of the
+    oracle."""
+    m, n, k = 2048, 5120, 1024
+    blocks, w = quantized(Q4_K, n, k, 31)
+    x = activations(m, k, 31, torch.bfloat16).cuda()
+    wq = torch.from_numpy(blocks).cuda()
+    b = torch.from_numpy(np.random.default_rng(31).standard_normal(n, dtype=np.float32)).cuda()
+    print(f"gemm Q4_K tail split [{n},{k}] m={m}", flush=True)
+    ws = torch.empty(gemm_workspace_bytes(Q4_K, m, k), dtype=torch.uint8, device="cuda")
+    y1 = gguf_gemm(x, wq, Q4_K, (n, k), bias=b, workspace=ws).cpu()
+    y2 = gguf_gemm(x, wq, Q4_K, (n, k), bias=b, workspace=ws).cpu()
+    assert torch.equal(y1, y2)
+    ws_min = torch.empty(_q4k_ws_required(m, k), dtype=torch.uint8, device="cuda")
+    y3 = gguf_gemm(x, wq, Q4_K, (n, k), bias=b, workspace=ws_min).cpu()
+    ref = matmul_ref.linear_ref(x.cpu().float().numpy(), w) + b.cpu().numpy()
+    check_close(y1.numpy(), ref, f"gemm Q4_K tail split [{n},{k}] m={m}")
+    check_close(y3.numpy(), ref, f"gemm Q4_K unsplit [{n},{k}] m={m}")
+    # the whole tiles' columns are the unsplit launch's bits
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    full = (8 * 40 // cus) * cus  # whole rounds of the 8 x 40 tiles
+    nt = full // 8 * 128
+    assert torch.equal(y1[:, :nt], y3[:, :nt])
+
+
 def test_gemm_q4k_m2048_bias_via_linear():
     blocks, w = quantized(Q4_K, 1024, 2048, 13)
     x = activations(2048, 2048, 13, torch.bfloat16)

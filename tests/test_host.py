@@ -82,10 +82,11 @@ def test_error_codes_before_launch():
     # prefill GEMM workspace: Q4_K needs f16 activations + three planes of 32-element sums + row scales
     al = lambda v: (v + 255) // 256 * 256  # noqa: E731
     need = al(512 * 4096 * 2) + al(3 * 512 * 128 * 2) + al(512 * 4)
-    # + room for split-K partial sums: S x N <= 128 x 256 / ceil(M / 256) at M <= 1024
+    # + room for split-K partial sums: S x N <= 128 x 256 / ceil(M / 256) (a few tiles split along K,
+    # or a grid's partial last round split)
     assert lib.draco_gguf_gemm_workspace_size(12, 512, 4096) == need + 512 * 128 * 128 * 4
     assert lib.draco_gguf_gemm_workspace_size(12, 2048, 4096) == (al(2048 * 4096 * 2) + al(3 * 2048 * 128 * 2) +
-                                                                  al(2048 * 4))
+                                                                  al(2048 * 4) + 2048 * 128 * 32 * 4)
     assert lib.draco_gguf_gemm_workspace_size(8, 512, 4096) == 0
     assert lib.draco_gguf_gemm_workspace_size(99, 512, 4096) == 0
     gemm = lib.draco_gguf_gemm

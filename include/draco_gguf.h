@@ -158,9 +158,10 @@ int draco_gguf_gemv_residual_ws(int ggml_type, const void* w, size_t w_bytes, co
  * length k with this weight type (0 when the type's GEMM needs none).  Q4_K
  * requires m * k * 2 + 3 * m * (k / 32) * 2 + m * 4 bytes (rounded up to 256
  * per part: the activations as float16, their 32-element sums, the row
- * scales); for m <= 1024 the size returned adds m * 128 * (256 / ceil(m /
- * 256)) * 4 bytes of room for split-K partial sums, which shapes with too few
- * output tiles to fill the GPU use when the workspace given holds them.
+ * scales); the size returned adds m * 128 * (256 / ceil(m / 256)) * 4
+ * bytes of room for split-K partial sums, which shapes with too few output
+ * tiles to fill the GPU, and the partial last round of a grid that does not
+ * divide evenly over the CUs, use when the workspace given holds them.
  */
 size_t draco_gguf_gemm_workspace_size(int ggml_type, int64_t m, int64_t k);
 

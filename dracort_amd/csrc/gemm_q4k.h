@@ -107,33 +107,36 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const uint16_t* __restri
   int t = 0;
   if (mx > 0.f && __builtin_isfinite(mx)) t = ilogbf(mx) - 14;
 
+  // one 16-byte chunk (8 elements) per thread, so the loads and stores of a
+  // wave are contiguous; a 32-element group is four neighbouring lanes, whose
+  // partial sums meet in two exchanges ((s0 + s1) + (s2 + s3))
   const size_t plane = (size_t)M * groups;
-  for (int g = tid; g < groups; g += 256) {
-    uint32_t h[16];
+  uint4* const dst = reinterpret_cast<uint4*>(ws.xh + (size_t)m * K);
+  for (int c = tid; c < chunks; c += 256) {  // chunks is a multiple of 4: whole groups per pass
+    const uint4 v = xr[c];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t h[4];
     float sum = 0.f;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint4 v = xr[g * 4 + c];
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float f0 = ldexpf(__uint_as_float(w[i] << 16), -t), f1 = ldexpf(__uint_as_float(w[i] & 0xFFFF0000u), -t);
-        sum += f0;
-        sum += f1;
-        h[4 * c + i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f0, f1));
-      }
+    for (int i = 0; i < 4; ++i) {
+      const float f0 = ldexpf(__uint_as_float(w[i] << 16), -t), f1 = ldexpf(__uint_as_float(w[i] & 0xFFFF0000u), -t);
+      sum += f0;
+      sum += f1;
+      h[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f0, f1));
     }
-    uint4* dst = reinterpret_cast<uint4*>(ws.xh + (size_t)m * K + 32 * g);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) dst[c] = uint4{h[4 * c], h[4 * c + 1], h[4 * c + 2], h[4 * c + 3]};
-    const uint32_t hi = gq_bf16_rne(sum);
-    const float r1 = sum - __uint_as_float(hi << 16);
-    const uint32_t mid = gq_bf16_rne(r1);
-    const uint32_t lo = gq_bf16_rne(r1 - __uint_as_float(mid << 16));
-    const size_t o = (size_t)m * groups + g;
-    ws.sp[o] = (uint16_t)hi;
-    ws.sp[plane + o] = (uint16_t)mid;
-    ws.sp[2 * plane + o] = (uint16_t)lo;
+    dst[c] = uint4{h[0], h[1], h[2], h[3]};
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    if ((c & 3) == 0) {
+      const uint32_t hi = gq_bf16_rne(sum);
+      const float r1 = sum - __uint_as_float(hi << 16);
+      const uint32_t mid = gq_bf16_rne(r1);
+      const uint32_t lo = gq_bf16_rne(r1 - __uint_as_float(mid << 16));
+      const size_t o = (size_t)m * groups + (c >> 2);
+      ws.sp[o] = (uint16_t)hi;
+      ws.sp[plane + o] = (uint16_t)mid;
+      ws.sp[2 * plane + o] = (uint16_t)lo;
+    }
   }
   if (tid == 0) ws.rsc[m] = ldexpf(1.f, t);
 }

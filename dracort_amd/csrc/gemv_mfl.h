@@ -24,7 +24,8 @@
 
 namespace draco {
 
-constexpr int kMflMaxRowBytes = 16 * 144;  // Q4_K rows of K <= 4096
+constexpr int kMflMaxRowBytes = 16 * 144;   // Q4_K rows of K <= 4096
+constexpr int kMfl6MaxRowBytes = 16 * 210;  // Q6_K rows of K <= 4096
 
 // LDS bytes of one matrix's tile image for this row length.
 __host__ __device__ constexpr int mfl_tile_lds(int row_bytes) { return 16 * (row_bytes + 16); }
@@ -132,12 +133,111 @@ __device__ __forceinline__ void mfl_stream_q4k(const typename MfpTypes<kQ4_K>::X
   }
 }
 
-// The decode GEMV of 2..16 bf16 token rows over Q4_K matrices with K <= 4096
-// (gemv_mfp_kernel's jobs, modes and results).
-template <int MODE, int W>
+// The same for one Q6_K matrix (K a multiple of 2048 so a row is whole
+// 16-byte pieces): the 210-byte super-blocks sit at even offsets of the LDS
+// row, so each dword field is read as the two aligned dwords around it and
+// realigned (v_alignbyte); the chunk math is mf_chunk_q6, gemv_mfp_kernel's.
+template <bool DL, int W, class TileBase, class Emit>
+__device__ __forceinline__ void mfl_stream_q6k(const typename MfpTypes<kQ6_K>::X (&xr)[16 / W], int chunks,
+                                               int ntiles, int row_bytes, TileBase tile_base, Emit emit,
+                                               uint8_t* __restrict__ wl, mf_f32x4 (&part)[W][1][64]) {
+  constexpr int NT = W * 64, CPW = 16 / W;
+  constexpr int PPT = (kMfl6MaxRowBytes + NT - 1) / NT;  // pieces per thread: 16 x row_bytes / 16 bytes
+  constexpr int QL = DL ? 0 : 2, QH = DL ? 128 : 130, SC = DL ? 192 : 194, D = DL ? 208 : 0;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4, nl = lane & 15;
+  const int rs_bytes = row_bytes + 16;
+  const int ppr = row_bytes >> 4, pieces = row_bytes;
+
+  int dst[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    const int pc = tid + NT * j;
+    const int row = pc / ppr;
+    dst[j] = pc < pieces ? row * rs_bytes + ((pc - row * ppr) << 4) : -1;
+  }
+  uint4 stg[PPT];
+  auto issue = [&](int i) {
+    const MfRow t = tile_base(min(i, ntiles - 1), 0);
+    const __amdgpu_buffer_rsrc_t rs = i < ntiles ? t.rs : make_rsrc(nullptr, 0u);
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int pc = tid + NT * j;
+      const uint32_t off = pc < pieces ? (uint32_t)t.rowoff + ((uint32_t)pc << 4) : 0x80000000u;
+      typedef int v4i __attribute__((ext_vector_type(4)));
+      const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+      stg[j] = uint4{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+    }
+  };
+  auto commit = [&]() {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j)
+      if (dst[j] >= 0) *reinterpret_cast<uint4*>(wl + dst[j]) = stg[j];
+  };
+
+  if (ntiles <= 0) return;
+  issue(0);
+  commit();
+  issue(1);
+  __syncthreads();
+  for (int i = 0; i < ntiles; ++i) {
+    mf_f32x4 acc[1] = {mf_f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const int cc = ks + W * j;
+      if (cc < chunks) {
+        const uint8_t* rp = wl + nl * rs_bytes;
+        const int base = cc * 210;
+        // the four bytes at row offset o (even) from the aligned dwords around them
+        auto dw = [&](int o) -> uint32_t {
+          const uint32_t* w = reinterpret_cast<const uint32_t*>(rp + (o & ~3));
+          return __builtin_amdgcn_alignbyte(w[1], w[0], (uint32_t)(o & 3));
+        };
+        MfQ6 wc[1];
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) wc[0].ql[4 * n + 2 * tb + h] = dw(base + QL + 64 * n + 32 * tb + 16 * h + 4 * q);
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) wc[0].qh[2 * n + h] = dw(base + QH + 32 * n + 16 * h + 4 * q);
+        wc[0].sc = uint4{dw(base + SC), dw(base + SC + 4), dw(base + SC + 8), dw(base + SC + 12)};
+        wc[0].d = dw(base + D) & 0xFFFFu;
+        mf_chunk_q6<1>(xr[j], wc, acc);
+      }
+    }
+    part[ks][0][lane] = acc[0];
+    __syncthreads();  // tile i read by every wave, its partial tiles written
+    if (ks == 0) {
+      mf_f32x4 tot[1];
+      tot[0] = part[0][0][lane];
+#pragma unroll
+      for (int w = 1; w < W; ++w) {
+        const mf_f32x4 pp = part[w][0][lane];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tot[0][v] += pp[v];
+      }
+      emit(i, tot);
+    }
+    if (i + 1 < ntiles) {
+      commit();      // tile i + 1
+      issue(i + 2);  // an empty resource past the last tile
+    }
+    __syncthreads();  // tile i + 1 in LDS, the partial tiles free again
+  }
+}
+
+// The decode GEMV of 2..16 bf16 token rows over Q4_K (or single Q6_K)
+// matrices with K <= 4096 (gemv_mfp_kernel's jobs, modes and results).
+template <int QT, bool DL, int MODE, int W>
 __global__ __launch_bounds__(W * 64) void gemv_mfl_kernel(StreamJob job) {
   constexpr int NR = MODE == kSwiGLU ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) uint8_t wl[NR * mfl_tile_lds(kMflMaxRowBytes)];
+  static_assert(QT == kQ4_K || (QT == kQ6_K && NR == 1), "Q4_K, or one Q6_K matrix per row");
+  __shared__ __attribute__((aligned(16))) uint8_t wl[NR * mfl_tile_lds(QT == kQ6_K ? kMfl6MaxRowBytes : kMflMaxRowBytes)];
   __shared__ mf_f32x4 part[W][NR][64];
   const int lane = threadIdx.x & 63;
   const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -147,8 +247,8 @@ __global__ __launch_bounds__(W * 64) void gemv_mfl_kernel(StreamJob job) {
   const int ntiles = job.rows >> 4;
   const int my_tiles = ntiles > (int)blockIdx.x ? (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
 
-  typename MfpTypes<kQ4_K>::X xr[16 / W];
-  mfp_load_x<kQ4_K, W>(static_cast<const uint16_t*>(job.x) + (size_t)min(nl, M - 1) * k, chunks, ks, q, xr);
+  typename MfpTypes<QT>::X xr[16 / W];
+  mfp_load_x<QT, W>(static_cast<const uint16_t*>(job.x) + (size_t)min(nl, M - 1) * k, chunks, ks, q, xr);
 
   int c1 = INT_MAX, c2 = INT_MAX, c3 = INT_MAX;
   if constexpr (MODE == kPlain) {
@@ -214,16 +314,19 @@ __global__ __launch_bounds__(W * 64) void gemv_mfl_kernel(StreamJob job) {
       }
     }
   };
-  mfl_stream_q4k<NR, W>(xr, chunks, my_tiles, row_bytes, tile_base, emit, wl, part);
+  if constexpr (QT == kQ6_K)
+    mfl_stream_q6k<DL, W>(xr, chunks, my_tiles, row_bytes, tile_base, emit, wl, part);
+  else
+    mfl_stream_q4k<NR, W>(xr, chunks, my_tiles, row_bytes, tile_base, emit, wl, part);
 }
 
-template <int MODE, int W>
+template <int QT, bool DL, int MODE, int W>
 static int launch_gemv_mfl(const StreamJob& job, int blocks_per_cu, hipStream_t s) {
-  if (job.k > 4096 || job.k % 256 != 0 || job.rows % 16 != 0)
+  if (job.k > 4096 || job.k % (QT == kQ6_K ? 2048 : 256) != 0 || job.rows % 16 != 0)
     return set_error(DRACO_EINVAL_SHAPE, "LDS-staged matrix-core GEMV takes K <= 4096 and whole 16-row tiles");
   const int tiles = job.rows / 16;
   const int blocks = std::max(1, std::min(tiles, device_cus() * blocks_per_cu));
-  hipLaunchKernelGGL((gemv_mfl_kernel<MODE, W>), dim3(blocks), dim3(W * 64), 0, s, job);
+  hipLaunchKernelGGL((gemv_mfl_kernel<QT, DL, MODE, W>), dim3(blocks), dim3(W * 64), 0, s, job);
   return check_launch("gemv_mfl");
 }
 
@@ -235,13 +338,18 @@ static int gemv_mfma_dispatch(int qtype, bool d_last, const StreamJob& job, bool
   // (SwiGLU's two weight sets fit the 512-thread register budget for Q4_K only)
   if (xbf16 && job.k <= 4096 && (MODE != kSwiGLU || qtype == kQ4_K)) {
     if constexpr (MODE != kSwiGLU) {
+      // Q6_K rows of whole 16-byte pieces (K a multiple of 2048) through LDS
+      // as well; other lengths read their tiles straight into registers
+      if (qtype == kQ6_K && job.k % 2048 == 0)
+        return d_last ? launch_gemv_mfl<kQ6_K, true, MODE, 8>(job, 1, s)
+                      : launch_gemv_mfl<kQ6_K, false, MODE, 8>(job, 1, s);
       if (qtype == kQ6_K)
         return d_last ? launch_gemv_mfp<kQ6_K, true, MODE, 8>(job, 1, s)
                       : launch_gemv_mfp<kQ6_K, false, MODE, 8>(job, 1, s);
     }
     // Q4_K: the LDS-staged form above, bit-identical and faster (measured at
     // 16 rows: gate/up 33.1 -> 28.4 us, q/k/v 12.6 -> 11.5, o 11.1 -> 9.6)
-    if (qtype == kQ4_K) return launch_gemv_mfl<MODE, 8>(job, 1, s);
+    if (qtype == kQ4_K) return launch_gemv_mfl<kQ4_K, false, MODE, 8>(job, 1, s);
     if constexpr (MODE != kSwiGLU) return launch_gemv_mfp<kQ4_0, false, MODE, 8>(job, 1, s);
   }
   if (qtype == kQ6_K)

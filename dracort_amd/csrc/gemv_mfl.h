@@ -30,107 +30,155 @@ constexpr int kMfl6MaxRowBytes = 16 * 210;  // Q6_K rows of K <= 4096
 // LDS bytes of one matrix's tile image for this row length.
 __host__ __device__ constexpr int mfl_tile_lds(int row_bytes) { return 16 * (row_bytes + 16); }
 
-// Streams ntiles 16-row tiles of NR Q4_K matrices through the LDS image `wl`
-// (NR x mfl_tile_lds(row_bytes) bytes) against the wave's resident
-// activations xr.  tile_base(i, r) gives matrix r's buffer resource and the
+// Streams ntiles 16-row tiles of NR Q4_K matrices (rows of `chunks`
+// 256-element chunks, row_bytes = 144 chunks) through LDS against the wave's
+// resident activations xr, in units of W chunks of the tile's 16 rows (unit
+// j of a tile: chunks W j .. W j + W - 1, one per wave; U = chunks / W units
+// per tile, rounded up).  Units alternate between two LDS images (`wl`: 2 x
+// NR x mfl_unit_lds(W) bytes) and two register staging slots: a wave
+// multiplies unit v from its image, writes unit v + 1 (landed in registers)
+// to the other image, requests unit v + 3 into the freed slot and meets the
+// other waves at one barrier per unit.  A tile's partial 16 x 16 results go
+// to part[tile parity] and are summed by wave 0 after the barrier, while the
+// other waves go on; tile_base(i, r) gives matrix r's buffer resource and the
 // byte offset of tile i's first row; emit(i, tot) runs on wave 0 with tile
 // i's summed 16 x 16 result.
-template <int NR, int W, class TileBase, class Emit>
-__device__ __forceinline__ void mfl_stream_q4k(const typename MfpTypes<kQ4_K>::X (&xr)[16 / W], int chunks,
-                                               int ntiles, int row_bytes, TileBase tile_base, Emit emit,
-                                               uint8_t* __restrict__ wl, mf_f32x4 (&part)[W][NR][64]) {
+template <int NR, int W, int U, class TileBase, class Emit>
+__device__ __forceinline__ void mfl_stream_q4k_u(const typename MfpTypes<kQ4_K>::X (&xr)[16 / W], int chunks,
+                                                 int ntiles, int row_bytes, TileBase tile_base, Emit emit,
+                                                 uint8_t* __restrict__ wl, mf_f32x4 (&part)[2][W][NR][64]) {
   constexpr int NT = W * 64, CPW = 16 / W;
-  constexpr int PPT = (kMflMaxRowBytes + NT - 1) / NT;  // pieces per thread: 16 x row_bytes / 16 bytes
+  static_assert(U >= 1 && U <= CPW, "units per tile");
+  constexpr int UB = W * 144;                  // bytes of one row's span in a unit
+  constexpr int PPR = UB / 16;                 // 16-byte pieces per row and unit
+  constexpr int PPT = (16 * PPR + NT - 1) / NT;  // pieces per thread and matrix
+  constexpr int RS = UB + 16, IMG = 16 * RS;   // LDS row stride (16 bytes of padding), image per matrix
   const int tid = threadIdx.x, lane = tid & 63;
   const int ks = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane >> 4, nl = lane & 15;
-  const int rs_bytes = row_bytes + 16, img = 16 * rs_bytes;
-  const int ppr = row_bytes >> 4, pieces = row_bytes;  // pieces per row, per tile
+  const int nunits = ntiles * U;
 
-  // this thread's pieces: the same LDS destinations for every tile
-  int dst[PPT];
+  float sx[CPW][2];  // the resident chunks' group sums
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) mf_group_sums(xr[j], q, sx[j]);
+
+  // this thread's pieces: row, 16-byte column within the unit's span, LDS destination
+  int prow[PPT], pcol[PPT], dst[PPT];
 #pragma unroll
   for (int j = 0; j < PPT; ++j) {
     const int pc = tid + NT * j;
-    const int row = pc / ppr;
-    dst[j] = pc < pieces ? row * rs_bytes + ((pc - row * ppr) << 4) : -1;
+    prow[j] = pc / PPR;
+    pcol[j] = pc - prow[j] * PPR;
+    dst[j] = pc < 16 * PPR ? prow[j] * RS + (pcol[j] << 4) : -1;
   }
-  uint4 stg[NR][PPT];
-  // offsets past the end of a resource read zero without touching memory
-  auto issue = [&](int i) {
+  uint4 stg[2][NR][PPT];
+  // unit v into staging slot S; past the last unit (or a column past the
+  // row's chunks) an empty resource / an offset past the end reads zero
+  auto issue = [&](int v, uint4 (&sl)[NR][PPT]) {
+    const int i = min(v / U, ntiles - 1), uj = v - (v / U) * U;
+    const int span = min(chunks - W * uj, W) * 9;  // pieces per row in this unit
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      const MfRow t = tile_base(min(i, ntiles - 1), r);
-      const __amdgpu_buffer_rsrc_t rs = i < ntiles ? t.rs : make_rsrc(nullptr, 0u);
+      const MfRow t = tile_base(i, r);
+      const __amdgpu_buffer_rsrc_t rs = v < nunits ? t.rs : make_rsrc(nullptr, 0u);
 #pragma unroll
       for (int j = 0; j < PPT; ++j) {
-        const int pc = tid + NT * j;
-        const uint32_t off = pc < pieces ? (uint32_t)t.rowoff + ((uint32_t)pc << 4) : 0x80000000u;
+        const bool ok = dst[j] >= 0 && pcol[j] < span;
+        const uint32_t off = ok ? (uint32_t)(t.rowoff + prow[j] * row_bytes + uj * UB + (pcol[j] << 4)) : 0x80000000u;
         typedef int v4i __attribute__((ext_vector_type(4)));
-        const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-        stg[r][j] = uint4{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+        const v4i x4 = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+        sl[r][j] = uint4{(uint32_t)x4.x, (uint32_t)x4.y, (uint32_t)x4.z, (uint32_t)x4.w};
       }
     }
   };
-  auto commit = [&]() {
+  auto commit = [&](const uint4 (&sl)[NR][PPT], uint8_t* img) {
 #pragma unroll
     for (int r = 0; r < NR; ++r)
 #pragma unroll
       for (int j = 0; j < PPT; ++j)
-        if (dst[j] >= 0) *reinterpret_cast<uint4*>(wl + r * img + dst[j]) = stg[r][j];
+        if (dst[j] >= 0) *reinterpret_cast<uint4*>(img + r * IMG + dst[j]) = sl[r][j];
   };
 
   if (ntiles <= 0) return;
-  issue(0);
-  commit();
-  issue(1);
+  issue(0, stg[0]);
+  issue(1, stg[1]);
+  commit(stg[0], wl);
+  issue(2, stg[0]);
   __syncthreads();
-  for (int i = 0; i < ntiles; ++i) {
-    mf_f32x4 acc[NR];
+  mf_f32x4 acc[NR];
+  // units in pairs so that the staging slot (v % 2) and, for U = 2, the unit
+  // within its tile are compile-time constants
+  for (int v0 = 0; v0 < nunits; v0 += 2) {
 #pragma unroll
-    for (int r = 0; r < NR; ++r) acc[r] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int sl = 0; sl < 2; ++sl) {
+      const int v = v0 + sl;
+      const int i = U == 2 ? v0 / 2 : v;     // tile
+      const int uj = U == 2 ? sl : 0;        // unit within the tile (static for U = 2, 1)
+      const bool live = v < nunits;
+      const bool last = uj == U - 1;
+      const int pi = i & 1;                  // partial-tile buffer of this tile
+      if (live) {
+        if (uj == 0)
 #pragma unroll
-    for (int j = 0; j < CPW; ++j) {
-      const int cc = ks + W * j;
-      if (cc < chunks) {
-        MfChunk<kQ4_K> wc[NR];
+          for (int r = 0; r < NR; ++r) acc[r] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+        const int cc = W * uj + ks;
+        if (cc < chunks) {
+          MfChunk<kQ4_K> wc[NR];
+#pragma unroll
+          for (int r = 0; r < NR; ++r) {
+            const uint8_t* rp = wl + sl * NR * IMG + r * IMG + nl * RS + ks * 144;
+            wc[r].head = *reinterpret_cast<const uint4*>(rp);
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+              const uint2 t = *reinterpret_cast<const uint2*>(rp + 16 + 32 * p + 8 * q);
+              wc[r].qs[p][0] = t.x;
+              wc[r].qs[p][1] = t.y;
+            }
+          }
+          // U = 2: unit sl uses resident chunk sl; U = 1: chunk 0
+          mf_chunk_q4k_sx<NR>(xr[U == 2 ? sl : 0], wc, q, acc, sx[U == 2 ? sl : 0]);
+        }
+        if (last)
+#pragma unroll
+          for (int r = 0; r < NR; ++r) part[pi][ks][r][lane] = acc[r];
+      }
+      // the other image was last read by unit v - 1, which every wave finished
+      // before the previous barrier
+      if (v + 1 < nunits) {
+        commit(stg[sl ^ 1], wl + (sl ^ 1) * NR * IMG);  // unit v + 1
+        issue(v + 3, stg[sl ^ 1]);                     // an empty resource past the last unit
+      }
+      __syncthreads();  // unit v + 1 in LDS; after a tile's last unit, its partial tiles written
+      if (live && last && ks == 0) {
+        // part[pi] is next written two tiles later, after a barrier wave 0 reaches only after this
+        mf_f32x4 tot[NR];
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-          const uint8_t* rp = wl + r * img + nl * rs_bytes + cc * 144;
-          wc[r].head = *reinterpret_cast<const uint4*>(rp);
+          tot[r] = part[pi][0][r][lane];
 #pragma unroll
-          for (int p = 0; p < 4; ++p) {
-            const uint2 t = *reinterpret_cast<const uint2*>(rp + 16 + 32 * p + 8 * q);
-            wc[r].qs[p][0] = t.x;
-            wc[r].qs[p][1] = t.y;
+          for (int w = 1; w < W; ++w) {
+            const mf_f32x4 pp = part[pi][w][r][lane];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tot[r][e] += pp[e];
           }
         }
-        mf_chunk_q4<kQ4_K, true, NR>(xr[j], wc, q, acc);
+        emit(i, tot);
       }
     }
-#pragma unroll
-    for (int r = 0; r < NR; ++r) part[ks][r][lane] = acc[r];
-    __syncthreads();  // tile i read by every wave, its partial tiles written
-    if (ks == 0) {
-      mf_f32x4 tot[NR];
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        tot[r] = part[0][r][lane];
-#pragma unroll
-        for (int w = 1; w < W; ++w) {
-          const mf_f32x4 pp = part[w][r][lane];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) tot[r][v] += pp[v];
-        }
-      }
-      emit(i, tot);
-    }
-    if (i + 1 < ntiles) {
-      commit();      // tile i + 1
-      issue(i + 2);  // an empty resource past the last tile
-    }
-    __syncthreads();  // tile i + 1 in LDS, the partial tiles free again
   }
+}
+
+// LDS bytes of one matrix's unit image (W chunks of 16 rows, rows padded by 16 bytes).
+__host__ __device__ constexpr int mfl_unit_lds(int w) { return 16 * (w * 144 + 16); }
+
+template <int NR, int W, class TileBase, class Emit>
+__device__ __forceinline__ void mfl_stream_q4k(const typename MfpTypes<kQ4_K>::X (&xr)[16 / W], int chunks,
+                                               int ntiles, int row_bytes, TileBase tile_base, Emit emit,
+                                               uint8_t* __restrict__ wl, mf_f32x4 (&part)[2][W][NR][64]) {
+  if (chunks > W)
+    mfl_stream_q4k_u<NR, W, 2>(xr, chunks, ntiles, row_bytes, tile_base, emit, wl, part);
+  else
+    mfl_stream_q4k_u<NR, W, 1>(xr, chunks, ntiles, row_bytes, tile_base, emit, wl, part);
 }
 
 // The same for one Q6_K matrix (K a multiple of 2048 so a row is whole
@@ -237,8 +285,8 @@ template <int QT, bool DL, int MODE, int W>
 __global__ __launch_bounds__(W * 64) void gemv_mfl_kernel(StreamJob job) {
   constexpr int NR = MODE == kSwiGLU ? 2 : 1;
   static_assert(QT == kQ4_K || (QT == kQ6_K && NR == 1), "Q4_K, or one Q6_K matrix per row");
-  __shared__ __attribute__((aligned(16))) uint8_t wl[NR * mfl_tile_lds(QT == kQ6_K ? kMfl6MaxRowBytes : kMflMaxRowBytes)];
-  __shared__ mf_f32x4 part[W][NR][64];
+  __shared__ __attribute__((aligned(16))) uint8_t wl[QT == kQ6_K ? mfl_tile_lds(kMfl6MaxRowBytes) : 2 * NR * mfl_unit_lds(W)];
+  __shared__ mf_f32x4 part[2][W][NR][64];
   const int lane = threadIdx.x & 63;
   const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int q = lane >> 4, nl = lane & 15;
@@ -315,7 +363,7 @@ __global__ __launch_bounds__(W * 64) void gemv_mfl_kernel(StreamJob job) {
     }
   };
   if constexpr (QT == kQ6_K)
-    mfl_stream_q6k<DL, W>(xr, chunks, my_tiles, row_bytes, tile_base, emit, wl, part);
+    mfl_stream_q6k<DL, W>(xr, chunks, my_tiles, row_bytes, tile_base, emit, wl, part[0]);
   else
     mfl_stream_q4k<NR, W>(xr, chunks, my_tiles, row_bytes, tile_base, emit, wl, part);
 }

@@ -6,11 +6,13 @@
 // v_mfma_f32_16x16x32_bf16: A = the activations (16 token rows x 32 k, rows
 // past M are zero), B = the codes of 16 weight rows (exact in bf16 as
 // 128 + code, one v_perm_b32 per pair), one MFMA per 32-element scale group
-// (a Q4_K sub-block, a Q4_0 block).  Each group's result is scaled on the
-// VALU:  acc += a * (D - (128 + off) S) + b * S,  where w = a (code - off) + b, S =
-// sum_k x (one more MFMA per group against B = all ones, shared by the
-// wave's weight rows).  float32 activations are split into three bf16
-// planes and take three MFMAs per group, against unbiased codes.
+// (a Q4_K sub-block, a Q4_0 block), whose C operand is -(128 + off) S (S =
+// sum_k x of the group, from one more MFMA against B = -(128 + off), shared by
+// the wave's weight rows), so it yields sum x (code - off) with the bias
+// cancelled.  w = a (code - off) + b per group; the scales are applied on the
+// VALU, the Q4_K mins (b = -dmin m_g) through one more MFMA chain per row.
+// float32 activations are split into three bf16 planes and take three MFMAs
+// per group, against unbiased codes.
 //
 // Grid: a workgroup owns TPW tiles of 16 weight rows; four waves per tile
 // split K (wave ks takes 256-element chunks ks, ks + 4, ...), reading their
@@ -183,40 +185,154 @@ __device__ __forceinline__ void mf_load_x(const void* __restrict__ xrow, int p, 
   }
 }
 
-// acc += the products of one 256-element chunk: activations x (per group, NP
-// bf16 planes) against NR weight rows' codes w.
-template <int QT, bool XBF16, int NR>
-__device__ __forceinline__ void mf_chunk_q4(const mf_bf16x8 (&x)[8][XBF16 ? 1 : 3], const MfChunk<QT> (&w)[NR],
-                                            int q, mf_f32x4 (&acc)[NR]) {
-  constexpr int NP = XBF16 ? 1 : 3;
-  const uint32_t ones[4] = {kOnePair, kOnePair, kOnePair, kOnePair};
-  const mf_bf16x8 bones = __builtin_bit_cast(mf_bf16x8, ones);
-  float a[NR][8], cb[NR][8];
-#pragma unroll
-  for (int r = 0; r < NR; ++r) mf_coeffs<QT>(w[r], a[r], cb[r]);
-  const mf_f32x4 z = {0.f, 0.f, 0.f, 0.f};
+// Group sums of one chunk's bf16 activations (x as the A operand of the 16 x 16
+// x 32 MFMA: lane (q, nl) holds token row nl, k-slice q of each group) in the A
+// layout of v_mfma_f32_16x16x4f32: sx[b] = sum of group 4b + q of token row nl.
+// Each lane adds its slice, the four slices meet across lanes l ^ 16, l ^ 32.
+__device__ __forceinline__ void mf_group_sums(const mf_bf16x8 (&x)[8][1], int q, float (&sx)[2]) {
+  float p[8];
 #pragma unroll
   for (int g = 0; g < 8; ++g) {
-    mf_f32x4 sg = z;
+    const uint4 u = __builtin_bit_cast(uint4, x[g][0]);
+    const uint32_t h[4] = {u.x, u.y, u.z, u.w};
+    float t = 0.f;
 #pragma unroll
-    for (int j = NP - 1; j >= 0; --j) sg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[g][j], bones, sg, 0, 0, 0);
+    for (int i = 0; i < 4; ++i) t += __uint_as_float(h[i] << 16) + __uint_as_float(h[i] & 0xFFFF0000u);
+    t += __shfl_xor(t, 16);
+    p[g] = t + __shfl_xor(t, 32);
+  }
+  sx[0] = q == 0 ? p[0] : q == 1 ? p[1] : q == 2 ? p[2] : p[3];
+  sx[1] = q == 0 ? p[4] : q == 1 ? p[5] : q == 2 ? p[6] : p[7];
+}
+
+// acc += the products of one 256-element chunk: activations x (per group, NP
+// bf16 planes) against NR weight rows' codes w; sx (SX): the chunk's group
+// sums from mf_group_sums.
+//
+// bf16 activations: the group sums come from an MFMA against B = -(128 + off)
+// in every element, so they arrive already times -(128 + off), and enter the
+// codes' MFMA as its C operand: dg = -(128 + off) S + sum x (128 + code) =
+// sum x (code - off), the code bias cancelled inside the matrix core before
+// anything is scaled.  Q4_K: the group scales are applied per group
+// (t += sc_g dg_g, sc_g the 6-bit integer) and d once per chunk; the min
+// term dmin sum_g m_g S_g is one more MFMA chain per row (B = m_g, exact in
+// bf16), scaled by dmin once per chunk.  Q4_0: acc += d_g dg_g.
+// float32 activations (three bf16 planes, codes without the bias): the group
+// sums against all-ones and the scales on the VALU per group.
+template <int QT, bool XBF16, int NR, bool SX>
+__device__ __forceinline__ void mf_chunk_q4_impl(const mf_bf16x8 (&x)[8][XBF16 ? 1 : 3], const MfChunk<QT> (&w)[NR],
+                                                 int q, mf_f32x4 (&acc)[NR], const float (&sx)[2]) {
+  const mf_f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (XBF16) {
+    // bf16 pairs (-128, -128) for Q4_K, (-136, -136) for Q4_0 (codes offset by 8)
+    constexpr uint32_t kNeg = QT == kQ4_K ? 0xC300C300u : 0xC308C308u;
+    const uint32_t negs[4] = {kNeg, kNeg, kNeg, kNeg};
+    const mf_bf16x8 bneg = __builtin_bit_cast(mf_bf16x8, negs);
+    if constexpr (QT == kQ4_K) {
+      float sc[NR][8], mn[NR][2];
+      uint32_t mw[NR][2];
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const mf_bf16x8 bc = XBF16 ? mf_codes<QT>(w[r], g, q) : mf_codes_exact<QT>(w[r], g, q);
-      mf_f32x4 dg = z;
+      for (int r = 0; r < NR; ++r) {
+        const uint32_t s0 = w[r].head.y, s1 = w[r].head.z, s2 = w[r].head.w;
+        const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, m_lo = s1 & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+        const uint32_t m_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
 #pragma unroll
-      for (int j = NP - 1; j >= 0; --j) dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[g][j], bc, dg, 0, 0, 0);
+        for (int g = 0; g < 8; ++g) sc[r][g] = ubyte_f(g < 4 ? sc_lo : sc_hi, g & 3);
+        if constexpr (SX) {
+          // B of the min MFMAs: m of groups q and 4 + q (row nl)
+          mn[r][0] = (float)((m_lo >> (8 * q)) & 0xFFu);
+          mn[r][1] = (float)((m_hi >> (8 * q)) & 0xFFu);
+        } else {
+          mw[r][0] = m_lo;
+          mw[r][1] = m_hi;
+        }
+      }
+      mf_f32x4 t[NR], t2[NR];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        // sum x * (code - off) = D - (bias + off) S, formed with one rounding
-        // before it is scaled (the bias must cancel here, not in the running sum)
-        const float bias = (XBF16 ? kCodeBias : 0.f) + MfOff<QT>::value;
-        const float xcode = fmaf(-bias, sg[v], dg[v]);
-        if constexpr (QT == kQ4_K) acc[r][v] = fmaf(cb[r][g], sg[v], acc[r][v]);
-        acc[r][v] = fmaf(a[r][g], xcode, acc[r][v]);
+      for (int g = 0; g < 8; ++g) {
+        const mf_f32x4 sgn = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[g][0], bneg, z, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const mf_f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[g][0], mf_codes<QT>(w[r], g, q), sgn, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) t[r][v] = g == 0 ? sc[r][g] * dg[v] : fmaf(sc[r][g], dg[v], t[r][v]);
+          if constexpr (!SX) {
+            // sum_g m_g (-128 S_g), from the group sums the codes' MFMA used
+            const float m = ubyte_f(mw[r][g >> 2], g & 3);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) t2[r][v] = g == 0 ? m * sgn[v] : fmaf(m, sgn[v], t2[r][v]);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const float d = f16_bits_to_f32(w[r].head.x), dmin = f16_bits_to_f32(w[r].head.x >> 16);
+        float dm = dmin * (1.f / 128.f);  // t2 = -128 sum_g m_g S_g
+        if constexpr (SX) {
+          // sum_g m_g S_g in one pass of the float32 matrix cores: A = the group sums
+          // (token row nl, group 4b + q), B = m (group 4b + q, weight row nl)
+          t2[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(sx[0], mn[r][0], z, 0, 0, 0);
+          t2[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(sx[1], mn[r][1], t2[r], 0, 0, 0);
+          dm = -dmin;
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[r][v] = fmaf(dm, t2[r][v], fmaf(d, t[r][v], acc[r][v]));
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        const mf_f32x4 sgn = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[g][0], bneg, z, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const mf_f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[g][0], mf_codes<QT>(w[r], g, q), sgn, 0, 0, 0);
+          const float d = f16_bits_to_f32(w[r].d[g]);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[r][v] = fmaf(d, dg[v], acc[r][v]);
+        }
+      }
+    }
+  } else {
+    constexpr int NP = 3;
+    const uint32_t ones[4] = {kOnePair, kOnePair, kOnePair, kOnePair};
+    const mf_bf16x8 bones = __builtin_bit_cast(mf_bf16x8, ones);
+    float a[NR][8], cb[NR][8];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) mf_coeffs<QT>(w[r], a[r], cb[r]);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      mf_f32x4 sg = z;
+#pragma unroll
+      for (int j = NP - 1; j >= 0; --j) sg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[g][j], bones, sg, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const mf_bf16x8 bc = mf_codes_exact<QT>(w[r], g, q);
+        mf_f32x4 dg = z;
+#pragma unroll
+        for (int j = NP - 1; j >= 0; --j) dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[g][j], bc, dg, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          // sum x * (code - off) = D - off S before it is scaled
+          const float xcode = fmaf(-MfOff<QT>::value, sg[v], dg[v]);
+          if constexpr (QT == kQ4_K) acc[r][v] = fmaf(cb[r][g], sg[v], acc[r][v]);
+          acc[r][v] = fmaf(a[r][g], xcode, acc[r][v]);
+        }
       }
     }
   }
+}
+
+template <int QT, bool XBF16, int NR>
+__device__ __forceinline__ void mf_chunk_q4(const mf_bf16x8 (&x)[8][XBF16 ? 1 : 3], const MfChunk<QT> (&w)[NR],
+                                            int q, mf_f32x4 (&acc)[NR]) {
+  const float none[2] = {0.f, 0.f};
+  mf_chunk_q4_impl<QT, XBF16, NR, false>(x, w, q, acc, none);
+}
+// The same with the chunk's group sums from mf_group_sums (Q4_K, bf16).
+template <int NR>
+__device__ __forceinline__ void mf_chunk_q4k_sx(const mf_bf16x8 (&x)[8][1], const MfChunk<kQ4_K> (&w)[NR], int q,
+                                                mf_f32x4 (&acc)[NR], const float (&sx)[2]) {
+  mf_chunk_q4_impl<kQ4_K, true, NR, true>(x, w, q, acc, sx);
 }
 
 // The three bf16 planes of a float32 value (hi, mid, lo: each the
@@ -329,29 +445,38 @@ __device__ __forceinline__ mf_s16x4 mf_codes_q6(const MfQ6& c, int g) {
   return __builtin_bit_cast(mf_s16x4, v);
 }
 
+// The group sums times -160 (an MFMA against B = -160, exact in bf16) are the
+// C operand of the codes' MFMA, so dg = sum x (q - 32) leaves the matrix core
+// with the bias cancelled; t += sc_g dg_g per group, times d once per chunk.
 template <int NR>
 __device__ __forceinline__ void mf_chunk_q6(const uint2 (&x)[16], const MfQ6 (&w)[NR], mf_f32x4 (&acc)[NR]) {
-  const uint32_t ones2[2] = {kOnePair, kOnePair};
-  const mf_s16x4 bones = __builtin_bit_cast(mf_s16x4, ones2);
-  float a[NR][16];
+  const uint32_t neg2[2] = {0xC320C320u, 0xC320C320u};  // bf16 (-160, -160)
+  const mf_s16x4 bneg = __builtin_bit_cast(mf_s16x4, neg2);
+  float sc[NR][16];
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
-    const float d = f16_bits_to_f32(w[r].d);
     const uint32_t sw[4] = {w[r].sc.x, w[r].sc.y, w[r].sc.z, w[r].sc.w};
 #pragma unroll
-    for (int g = 0; g < 16; ++g) a[r][g] = d * sbyte_f(sw[g >> 2], g & 3);
+    for (int g = 0; g < 16; ++g) sc[r][g] = sbyte_f(sw[g >> 2], g & 3);
   }
   const mf_f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  mf_f32x4 t[NR];
 #pragma unroll
   for (int g = 0; g < 16; ++g) {
     const mf_s16x4 av = __builtin_bit_cast(mf_s16x4, x[g]);
-    const mf_f32x4 sg = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bones, z, 0, 0, 0);
+    const mf_f32x4 sgn = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bneg, z, 0, 0, 0);
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      const mf_f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, mf_codes_q6(w[r], g), z, 0, 0, 0);
+      const mf_f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, mf_codes_q6(w[r], g), sgn, 0, 0, 0);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[r][v] = fmaf(a[r][g], fmaf(-(kCodeBias + 32.f), sg[v], dg[v]), acc[r][v]);
+      for (int v = 0; v < 4; ++v) t[r][v] = g == 0 ? sc[r][g] * dg[v] : fmaf(sc[r][g], dg[v], t[r][v]);
     }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const float d = f16_bits_to_f32(w[r].d);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[r][v] = fmaf(d, t[r][v], acc[r][v]);
   }
 }
 
@@ -545,6 +670,10 @@ __device__ __forceinline__ void mfp_stream(const typename MfpTypes<QT>::X (&xr)[
       }
     }
   };
+  float sx[CPW][2];  // Q4_K: the resident chunks' group sums
+  if constexpr (QT == kQ4_K)
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) mf_group_sums(xr[j], q, sx[j]);
   WChunk wb[2][CPW][NR];
   load_tile(0, wb[0]);
   for (int i0 = 0; i0 < ntiles; i0 += 2) {
@@ -562,6 +691,8 @@ __device__ __forceinline__ void mfp_stream(const typename MfpTypes<QT>::X (&xr)[
           if (ks + W * j < chunks) {
             if constexpr (QT == kQ6_K)
               mf_chunk_q6<NR>(xr[j], wb[p][j], acc);
+            else if constexpr (QT == kQ4_K)
+              mf_chunk_q4k_sx<NR>(xr[j], wb[p][j], q, acc, sx[j]);
             else
               mf_chunk_q4<QT, true, NR>(xr[j], wb[p][j], q, acc);
           }

@@ -1,66 +1,75 @@
-// Small-batch decode GEMV (2..16 activation rows) for Q4_K with the weight
-// tiles staged through LDS.
+// Small-batch decode GEMV (2..16 activation rows) for Q4_K and Q6_K with the
+// weight tiles staged through LDS.
 //
 // The chunk math is the persistent matrix-core GEMV's (gemv_mfma.h:
 // activations resident in registers for the launch, wave ks taking chunks
-// ks, ks + W, ...; one v_mfma_f32_16x16x32_bf16 per 32-weight group against
-// the codes as 128 + code, the group sums from one more MFMA, scales on the
-// VALU), and so are the results, bit for bit.  The weights reach the lanes
-// differently.  A lane's share of a 16-row tile in the MFMA layout is four
-// 8-byte pieces per chunk spread over 16 rows; loading that straight into
-// registers issues requests that each touch 16 rows (measured on MI355X:
-// with the math removed, a 2 x 14336 x 4096 launch moved 2.9 TB/s where a
-// plain read of the same bytes reaches 5.3).  Here the 16 rows of a tile,
-// one contiguous span of 16 x row_bytes, are read by the whole workgroup as
-// consecutive 16-byte pieces (piece p by thread p mod 512), written to an
-// LDS image with each row padded by 16 bytes (rows fall on different
-// banks), and the lanes read their pieces from there (4.4 TB/s with the
-// math removed).  One tile is in flight while the previous one is
-// multiplied: tile i + 2 is requested right after tile i + 1 is written to
-// LDS, two barriers per tile.
+// ks, ks + W, ...; one MFMA per scale group against the codes as 128 + code,
+// the bias cancelled through the MFMA's C operand), and so are the results,
+// bit for bit.  The weights reach the lanes differently.  A lane's share of
+// a 16-row tile in the MFMA layout is a few pieces per chunk spread over 16
+// rows; loading that straight into registers issues requests that each touch
+// 16 rows (measured on MI355X: with the math removed, a 2 x 14336 x 4096
+// launch moved 2.9 TB/s where a plain read of the same bytes reaches 5.3).
+// Here the tile is read by the whole workgroup as consecutive 16-byte pieces
+// of its 16 rows, written to an LDS image with each row padded by 16 bytes
+// (rows fall on different banks), and the lanes read their pieces from
+// there; see mfl_stream_u for the pipeline.
+//
+// The same stream serves the split-K form (gemv_mfl_split_kernel): one
+// workgroup per CU takes an equal run of (split, tile) units, holds the
+// split's activations in registers and writes raw partial sums that
+// gemv_split_sum_kernel adds in split order.
 #pragma once
 
 #include "gemv_mfma.h"
 
 namespace draco {
 
-constexpr int kMflMaxRowBytes = 16 * 144;   // Q4_K rows of K <= 4096
-constexpr int kMfl6MaxRowBytes = 16 * 210;  // Q6_K rows of K <= 4096
+// Bytes of one 256-element chunk of a row, and the LDS bytes of one matrix's
+// unit image (W chunks of 16 rows, rows padded by 16 bytes).
+template <int QT> struct MflChunk { static constexpr int bytes = QT == kQ6_K ? 210 : 144; };
+template <int QT>
+__host__ __device__ constexpr int mfl_unit_lds(int w) { return 16 * (w * MflChunk<QT>::bytes + 16); }
 
-// LDS bytes of one matrix's tile image for this row length.
-__host__ __device__ constexpr int mfl_tile_lds(int row_bytes) { return 16 * (row_bytes + 16); }
-
-// Streams ntiles 16-row tiles of NR Q4_K matrices (rows of `chunks`
-// 256-element chunks, row_bytes = 144 chunks) through LDS against the wave's
-// resident activations xr, in units of W chunks of the tile's 16 rows (unit
-// j of a tile: chunks W j .. W j + W - 1, one per wave; U = chunks / W units
-// per tile, rounded up).  Units alternate between two LDS images (`wl`: 2 x
-// NR x mfl_unit_lds(W) bytes) and two register staging slots: a wave
-// multiplies unit v from its image, writes unit v + 1 (landed in registers)
-// to the other image, requests unit v + 3 into the freed slot and meets the
-// other waves at one barrier per unit.  A tile's partial 16 x 16 results go
-// to part[tile parity] and are summed by wave 0 after the barrier, while the
-// other waves go on; tile_base(i, r) gives matrix r's buffer resource and the
-// byte offset of tile i's first row; emit(i, tot) runs on wave 0 with tile
-// i's summed 16 x 16 result.
-template <int NR, int W, int U, class TileBase, class Emit>
-__device__ __forceinline__ void mfl_stream_q4k_u(const typename MfpTypes<kQ4_K>::X (&xr)[16 / W], int chunks,
-                                                 int ntiles, int row_bytes, TileBase tile_base, Emit emit,
-                                                 uint8_t* __restrict__ wl, mf_f32x4 (&part)[2][W][NR][64]) {
+// Streams ntiles 16-row tiles of NR matrices (Q4_K, or one Q6_K matrix)
+// through LDS against the wave's resident activations xr.  A tile's rows
+// are `chunks` 256-element chunks long, starting at tile_base(i, r).rowoff
+// (matrix r's buffer resource, byte offset of tile i's first row plus any
+// chunk offset; rows row_bytes apart).  The tile is read in units of W
+// chunks of its 16 rows (unit j: chunks W j .. W j + W - 1, one per wave; U =
+// chunks / W units per tile, rounded up; Q6_K units are whole, W chunks of
+// 210 bytes being whole 16-byte pieces).  Units alternate between two LDS
+// images (`wl`: 2 x NR x mfl_unit_lds<QT>(W) bytes) and two register staging
+// slots: a wave multiplies unit v from its image, writes unit v + 1 (landed
+// in registers) to the other image, requests unit v + 3 into the freed slot
+// and meets the other waves at one barrier per unit.  A tile's partial
+// 16 x 16 results go to part[tile parity] and are summed by wave 0 after the
+// barrier, while the other waves go on; emit(i, tot) runs on wave 0 with
+// tile i's summed result.  Q6_K super-blocks sit at even LDS offsets, so
+// each dword field is read as the two aligned dwords around it and realigned
+// (v_alignbyte).
+template <int QT, bool DL, int NR, int W, int U, class TileBase, class Emit>
+__device__ __forceinline__ void mfl_stream_u(const typename MfpTypes<QT>::X (&xr)[16 / W], int chunks, int ntiles,
+                                             int row_bytes, TileBase tile_base, Emit emit, uint8_t* __restrict__ wl,
+                                             mf_f32x4 (&part)[2][W][NR][64]) {
   constexpr int NT = W * 64, CPW = 16 / W;
   static_assert(U >= 1 && U <= CPW, "units per tile");
-  constexpr int UB = W * 144;                  // bytes of one row's span in a unit
-  constexpr int PPR = UB / 16;                 // 16-byte pieces per row and unit
+  static_assert(QT == kQ4_K || (QT == kQ6_K && NR == 1 && (W * 210) % 16 == 0), "Q4_K, or one Q6_K matrix");
+  constexpr int CB = MflChunk<QT>::bytes;
+  constexpr int UB = W * CB;                     // bytes of one row's span in a unit
+  constexpr int PPR = UB / 16;                   // 16-byte pieces per row and unit
   constexpr int PPT = (16 * PPR + NT - 1) / NT;  // pieces per thread and matrix
-  constexpr int RS = UB + 16, IMG = 16 * RS;   // LDS row stride (16 bytes of padding), image per matrix
+  constexpr int RS = UB + 16, IMG = 16 * RS;     // LDS row stride, image per matrix
+  constexpr int QL = DL ? 0 : 2, QH = DL ? 128 : 130, SC = DL ? 192 : 194, D = DL ? 208 : 0;
   const int tid = threadIdx.x, lane = tid & 63;
   const int ks = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane >> 4, nl = lane & 15;
   const int nunits = ntiles * U;
 
-  float sx[CPW][2];  // the resident chunks' group sums
+  float sx[CPW][2];  // Q4_K: the resident chunks' group sums
+  if constexpr (QT == kQ4_K)
 #pragma unroll
-  for (int j = 0; j < CPW; ++j) mf_group_sums(xr[j], q, sx[j]);
+    for (int j = 0; j < CPW; ++j) mf_group_sums(xr[j], q, sx[j]);
 
   // this thread's pieces: row, 16-byte column within the unit's span, LDS destination
   int prow[PPT], pcol[PPT], dst[PPT];
@@ -72,11 +81,11 @@ __device__ __forceinline__ void mfl_stream_q4k_u(const typename MfpTypes<kQ4_K>:
     dst[j] = pc < 16 * PPR ? prow[j] * RS + (pcol[j] << 4) : -1;
   }
   uint4 stg[2][NR][PPT];
-  // unit v into staging slot S; past the last unit (or a column past the
+  // unit v into a staging slot; past the last unit (or a column past the
   // row's chunks) an empty resource / an offset past the end reads zero
   auto issue = [&](int v, uint4 (&sl)[NR][PPT]) {
     const int i = min(v / U, ntiles - 1), uj = v - (v / U) * U;
-    const int span = min(chunks - W * uj, W) * 9;  // pieces per row in this unit
+    const int span = (min(chunks - W * uj, W) * CB) >> 4;  // pieces per row in this unit
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       const MfRow t = tile_base(i, r);
@@ -106,37 +115,62 @@ __device__ __forceinline__ void mfl_stream_q4k_u(const typename MfpTypes<kQ4_K>:
   issue(2, stg[0]);
   __syncthreads();
   mf_f32x4 acc[NR];
-  // units in pairs so that the staging slot (v % 2) and, for U = 2, the unit
-  // within its tile are compile-time constants
+  // units in pairs so that the staging slot and image (v % 2) and, for U = 2,
+  // the unit within its tile are compile-time constants
   for (int v0 = 0; v0 < nunits; v0 += 2) {
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl) {
       const int v = v0 + sl;
-      const int i = U == 2 ? v0 / 2 : v;     // tile
-      const int uj = U == 2 ? sl : 0;        // unit within the tile (static for U = 2, 1)
+      const int i = U == 2 ? v0 / 2 : v;  // tile
+      const int uj = U == 2 ? sl : 0;     // unit within the tile
       const bool live = v < nunits;
       const bool last = uj == U - 1;
-      const int pi = i & 1;                  // partial-tile buffer of this tile
+      const int pi = i & 1;  // partial-tile buffer of this tile
       if (live) {
         if (uj == 0)
 #pragma unroll
           for (int r = 0; r < NR; ++r) acc[r] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
-        const int cc = W * uj + ks;
-        if (cc < chunks) {
-          MfChunk<kQ4_K> wc[NR];
+        const int xj = U == 2 ? sl : 0;  // the resident chunk of this unit
+        if (W * uj + ks < chunks) {
+          const uint8_t* img = wl + sl * NR * IMG;
+          if constexpr (QT == kQ4_K) {
+            MfChunk<kQ4_K> wc[NR];
 #pragma unroll
-          for (int r = 0; r < NR; ++r) {
-            const uint8_t* rp = wl + sl * NR * IMG + r * IMG + nl * RS + ks * 144;
-            wc[r].head = *reinterpret_cast<const uint4*>(rp);
+            for (int r = 0; r < NR; ++r) {
+              const uint8_t* rp = img + r * IMG + nl * RS + ks * CB;
+              wc[r].head = *reinterpret_cast<const uint4*>(rp);
 #pragma unroll
-            for (int p = 0; p < 4; ++p) {
-              const uint2 t = *reinterpret_cast<const uint2*>(rp + 16 + 32 * p + 8 * q);
-              wc[r].qs[p][0] = t.x;
-              wc[r].qs[p][1] = t.y;
+              for (int p = 0; p < 4; ++p) {
+                const uint2 t = *reinterpret_cast<const uint2*>(rp + 16 + 32 * p + 8 * q);
+                wc[r].qs[p][0] = t.x;
+                wc[r].qs[p][1] = t.y;
+              }
             }
+            mf_chunk_q4k_sx<NR>(xr[xj], wc, q, acc, sx[xj]);
+          } else {
+            const uint8_t* rp = img + nl * RS;
+            const int base = ks * CB;
+            // the four bytes at row offset o (even) from the aligned dwords around them
+            auto dw = [&](int o) -> uint32_t {
+              const uint32_t* w = reinterpret_cast<const uint32_t*>(rp + (o & ~3));
+              return __builtin_amdgcn_alignbyte(w[1], w[0], (uint32_t)(o & 3));
+            };
+            MfQ6 wc[1];
+#pragma unroll
+            for (int n = 0; n < 2; ++n)
+#pragma unroll
+              for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                  wc[0].ql[4 * n + 2 * tb + h] = dw(base + QL + 64 * n + 32 * tb + 16 * h + 4 * q);
+#pragma unroll
+            for (int n = 0; n < 2; ++n)
+#pragma unroll
+              for (int h = 0; h < 2; ++h) wc[0].qh[2 * n + h] = dw(base + QH + 32 * n + 16 * h + 4 * q);
+            wc[0].sc = uint4{dw(base + SC), dw(base + SC + 4), dw(base + SC + 8), dw(base + SC + 12)};
+            wc[0].d = dw(base + D) & 0xFFFFu;
+            mf_chunk_q6<1>(xr[xj], wc, acc);
           }
-          // U = 2: unit sl uses resident chunk sl; U = 1: chunk 0
-          mf_chunk_q4k_sx<NR>(xr[U == 2 ? sl : 0], wc, q, acc, sx[U == 2 ? sl : 0]);
         }
         if (last)
 #pragma unroll
@@ -168,115 +202,22 @@ __device__ __forceinline__ void mfl_stream_q4k_u(const typename MfpTypes<kQ4_K>:
   }
 }
 
-// LDS bytes of one matrix's unit image (W chunks of 16 rows, rows padded by 16 bytes).
-__host__ __device__ constexpr int mfl_unit_lds(int w) { return 16 * (w * 144 + 16); }
+template <int QT, bool DL, int NR, int W, class TileBase, class Emit>
+__device__ __forceinline__ void mfl_stream(const typename MfpTypes<QT>::X (&xr)[16 / W], int chunks, int ntiles,
+                                           int row_bytes, TileBase tile_base, Emit emit, uint8_t* __restrict__ wl,
+                                           mf_f32x4 (&part)[2][W][NR][64]) {
+  if (chunks > W)
+    mfl_stream_u<QT, DL, NR, W, 2>(xr, chunks, ntiles, row_bytes, tile_base, emit, wl, part);
+  else
+    mfl_stream_u<QT, DL, NR, W, 1>(xr, chunks, ntiles, row_bytes, tile_base, emit, wl, part);
+}
 
+// The Q4_K form (the MoE up projection's stream).
 template <int NR, int W, class TileBase, class Emit>
 __device__ __forceinline__ void mfl_stream_q4k(const typename MfpTypes<kQ4_K>::X (&xr)[16 / W], int chunks,
                                                int ntiles, int row_bytes, TileBase tile_base, Emit emit,
                                                uint8_t* __restrict__ wl, mf_f32x4 (&part)[2][W][NR][64]) {
-  if (chunks > W)
-    mfl_stream_q4k_u<NR, W, 2>(xr, chunks, ntiles, row_bytes, tile_base, emit, wl, part);
-  else
-    mfl_stream_q4k_u<NR, W, 1>(xr, chunks, ntiles, row_bytes, tile_base, emit, wl, part);
-}
-
-// The same for one Q6_K matrix (K a multiple of 2048 so a row is whole
-// 16-byte pieces): the 210-byte super-blocks sit at even offsets of the LDS
-// row, so each dword field is read as the two aligned dwords around it and
-// realigned (v_alignbyte); the chunk math is mf_chunk_q6, gemv_mfp_kernel's.
-template <bool DL, int W, class TileBase, class Emit>
-__device__ __forceinline__ void mfl_stream_q6k(const typename MfpTypes<kQ6_K>::X (&xr)[16 / W], int chunks,
-                                               int ntiles, int row_bytes, TileBase tile_base, Emit emit,
-                                               uint8_t* __restrict__ wl, mf_f32x4 (&part)[W][1][64]) {
-  constexpr int NT = W * 64, CPW = 16 / W;
-  constexpr int PPT = (kMfl6MaxRowBytes + NT - 1) / NT;  // pieces per thread: 16 x row_bytes / 16 bytes
-  constexpr int QL = DL ? 0 : 2, QH = DL ? 128 : 130, SC = DL ? 192 : 194, D = DL ? 208 : 0;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int q = lane >> 4, nl = lane & 15;
-  const int rs_bytes = row_bytes + 16;
-  const int ppr = row_bytes >> 4, pieces = row_bytes;
-
-  int dst[PPT];
-#pragma unroll
-  for (int j = 0; j < PPT; ++j) {
-    const int pc = tid + NT * j;
-    const int row = pc / ppr;
-    dst[j] = pc < pieces ? row * rs_bytes + ((pc - row * ppr) << 4) : -1;
-  }
-  uint4 stg[PPT];
-  auto issue = [&](int i) {
-    const MfRow t = tile_base(min(i, ntiles - 1), 0);
-    const __amdgpu_buffer_rsrc_t rs = i < ntiles ? t.rs : make_rsrc(nullptr, 0u);
-#pragma unroll
-    for (int j = 0; j < PPT; ++j) {
-      const int pc = tid + NT * j;
-      const uint32_t off = pc < pieces ? (uint32_t)t.rowoff + ((uint32_t)pc << 4) : 0x80000000u;
-      typedef int v4i __attribute__((ext_vector_type(4)));
-      const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-      stg[j] = uint4{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
-    }
-  };
-  auto commit = [&]() {
-#pragma unroll
-    for (int j = 0; j < PPT; ++j)
-      if (dst[j] >= 0) *reinterpret_cast<uint4*>(wl + dst[j]) = stg[j];
-  };
-
-  if (ntiles <= 0) return;
-  issue(0);
-  commit();
-  issue(1);
-  __syncthreads();
-  for (int i = 0; i < ntiles; ++i) {
-    mf_f32x4 acc[1] = {mf_f32x4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int j = 0; j < CPW; ++j) {
-      const int cc = ks + W * j;
-      if (cc < chunks) {
-        const uint8_t* rp = wl + nl * rs_bytes;
-        const int base = cc * 210;
-        // the four bytes at row offset o (even) from the aligned dwords around them
-        auto dw = [&](int o) -> uint32_t {
-          const uint32_t* w = reinterpret_cast<const uint32_t*>(rp + (o & ~3));
-          return __builtin_amdgcn_alignbyte(w[1], w[0], (uint32_t)(o & 3));
-        };
-        MfQ6 wc[1];
-#pragma unroll
-        for (int n = 0; n < 2; ++n)
-#pragma unroll
-          for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) wc[0].ql[4 * n + 2 * tb + h] = dw(base + QL + 64 * n + 32 * tb + 16 * h + 4 * q);
-#pragma unroll
-        for (int n = 0; n < 2; ++n)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) wc[0].qh[2 * n + h] = dw(base + QH + 32 * n + 16 * h + 4 * q);
-        wc[0].sc = uint4{dw(base + SC), dw(base + SC + 4), dw(base + SC + 8), dw(base + SC + 12)};
-        wc[0].d = dw(base + D) & 0xFFFFu;
-        mf_chunk_q6<1>(xr[j], wc, acc);
-      }
-    }
-    part[ks][0][lane] = acc[0];
-    __syncthreads();  // tile i read by every wave, its partial tiles written
-    if (ks == 0) {
-      mf_f32x4 tot[1];
-      tot[0] = part[0][0][lane];
-#pragma unroll
-      for (int w = 1; w < W; ++w) {
-        const mf_f32x4 pp = part[w][0][lane];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) tot[0][v] += pp[v];
-      }
-      emit(i, tot);
-    }
-    if (i + 1 < ntiles) {
-      commit();      // tile i + 1
-      issue(i + 2);  // an empty resource past the last tile
-    }
-    __syncthreads();  // tile i + 1 in LDS, the partial tiles free again
-  }
+  mfl_stream<kQ4_K, false, NR, W>(xr, chunks, ntiles, row_bytes, tile_base, emit, wl, part);
 }
 
 // The decode GEMV of 2..16 bf16 token rows over Q4_K (or single Q6_K)
@@ -285,7 +226,7 @@ template <int QT, bool DL, int MODE, int W>
 __global__ __launch_bounds__(W * 64) void gemv_mfl_kernel(StreamJob job) {
   constexpr int NR = MODE == kSwiGLU ? 2 : 1;
   static_assert(QT == kQ4_K || (QT == kQ6_K && NR == 1), "Q4_K, or one Q6_K matrix per row");
-  __shared__ __attribute__((aligned(16))) uint8_t wl[QT == kQ6_K ? mfl_tile_lds(kMfl6MaxRowBytes) : 2 * NR * mfl_unit_lds(W)];
+  __shared__ __attribute__((aligned(16))) uint8_t wl[2 * NR * mfl_unit_lds<QT>(W)];
   __shared__ mf_f32x4 part[2][W][NR][64];
   const int lane = threadIdx.x & 63;
   const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -362,10 +303,58 @@ __global__ __launch_bounds__(W * 64) void gemv_mfl_kernel(StreamJob job) {
       }
     }
   };
-  if constexpr (QT == kQ6_K)
-    mfl_stream_q6k<DL, W>(xr, chunks, my_tiles, row_bytes, tile_base, emit, wl, part[0]);
-  else
-    mfl_stream_q4k<NR, W>(xr, chunks, my_tiles, row_bytes, tile_base, emit, wl, part);
+  mfl_stream<QT, DL, NR, W>(xr, chunks, my_tiles, row_bytes, tile_base, emit, wl, part);
+}
+
+// Split-K small-batch GEMV for one matrix with long rows (the batch-16 down
+// projection): K in splits of W chunks, units (split s, 16-row tile t) in
+// split-major order, workgroup b of G taking units [U b / G, U (b + 1) / G)
+// -- every CU the same number of tiles, the runs crossing a split boundary at
+// most once.  For each split of its run the workgroup loads that split's
+// activations (16 token rows x W chunks, one chunk per wave, rows past M
+// repeating row M - 1) into registers once and streams its tiles through
+// mfl_stream_u; each tile's raw 16 x 16 sums go to part[s] (M x n floats per
+// split), which gemv_split_sum_kernel adds in split order.  Q6_K needs
+// whole-W-chunk splits (K a multiple of 2048); n a multiple of 16.
+template <int QT, bool DL, int W>
+__global__ __launch_bounds__(W * 64) void gemv_mfl_split_kernel(StreamJob job) {
+  constexpr int CB = MflChunk<QT>::bytes;
+  __shared__ __attribute__((aligned(16))) uint8_t wl[2 * mfl_unit_lds<QT>(W)];
+  __shared__ mf_f32x4 part[2][W][1][64];
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, nl = lane & 15;
+  const int k = job.k, M = job.m, chunks = k >> 8;
+  const int n = job.n[0], tiles = n >> 4, row_bytes = job.row_bytes;
+  const int splits = (chunks + W - 1) / W;
+  const int units = splits * tiles;
+  const int G = gridDim.x, b = blockIdx.x;
+  const int u1 = (int)((int64_t)units * (b + 1) / G);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(job.w[0], (uint32_t)((int64_t)n * row_bytes));
+  const uint16_t* const x = static_cast<const uint16_t*>(job.x);
+  float* const out = job.part;
+  for (int u = (int)((int64_t)units * b / G); u < u1;) {
+    const int s = u / tiles, t0 = u - s * tiles;
+    const int nt = min(u1 - u, tiles - t0);
+    const int c0 = W * s, nch = min(W, chunks - c0);
+    typename MfpTypes<QT>::X xr[16 / W];
+    mfp_load_x<QT, W>(x + (size_t)min(nl, M - 1) * k + c0 * 256, nch, ks, q, xr);
+    auto tile_base = [=](int i, int) { return MfRow{rs, (t0 + i) * 16 * row_bytes + c0 * CB}; };
+    auto emit = [=](int i, const mf_f32x4 (&tot)[1]) {
+      float* const pp = out + (size_t)s * M * n + 16 * (t0 + i) + nl;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (4 * q + v < M) pp[(size_t)(4 * q + v) * n] = tot[0][v];
+    };
+    mfl_stream_u<QT, DL, 1, W, 1>(xr, nch, nt, row_bytes, tile_base, emit, wl, part);
+    u += nt;
+  }
+}
+
+// Whether gemv_mfl_split_kernel takes a split launch of this job.
+inline bool mfl_split_ok(int qtype, const StreamJob& job) {
+  return job.n_mats == 1 && job.rows % 16 == 0 && job.split_chunks == 8 &&
+         (qtype == kQ4_K || (qtype == kQ6_K && job.k % 2048 == 0));
 }
 
 template <int QT, bool DL, int MODE, int W>
@@ -378,8 +367,34 @@ static int launch_gemv_mfl(const StreamJob& job, int blocks_per_cu, hipStream_t 
   return check_launch("gemv_mfl");
 }
 
+// A split launch (job.part from gemv_split_bytes) through gemv_mfl_split_kernel,
+// one workgroup per CU (or per unit when there are fewer), then the ordered sum.
+template <int QT, bool DL, int MODE>
+static int launch_gemv_mfl_split(const StreamJob& job, hipStream_t s) {
+  const int splits = (job.k / 256 + 7) / 8;
+  const int units = splits * (job.rows / 16);
+  hipLaunchKernelGGL((gemv_mfl_split_kernel<QT, DL, 8>), dim3(std::max(1, std::min(units, device_cus()))), dim3(512),
+                     0, s, job);
+  if (int rc = check_launch("gemv_mfl_split")) return rc;
+  const size_t total = (size_t)job.m * job.n[0];
+  float* const y = MODE == kResid ? job.resid : job.y[0];
+  uint16_t* const yb = MODE == kResid ? job.resid_bf16 : job.yb[0];
+  hipLaunchKernelGGL(gemv_split_sum_kernel<MODE>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, job.part,
+                     splits, job.m, job.n[0], y, yb, job.bias);
+  return check_launch("gemv_split_sum");
+}
+
 template <int MODE>
 static int gemv_mfma_dispatch(int qtype, bool d_last, const StreamJob& job, bool xbf16, hipStream_t s) {
+  // long rows split over K with a workspace: the LDS-staged split form
+  // (measured on MI355X at 16 rows, 4096 x 14336 Q6_K: see gemv_mfl_split_kernel)
+  if constexpr (MODE != kSwiGLU) {
+    if (xbf16 && job.part && mfl_split_ok(qtype, job)) {
+      if (qtype == kQ6_K)
+        return d_last ? launch_gemv_mfl_split<kQ6_K, true, MODE>(job, s) : launch_gemv_mfl_split<kQ6_K, false, MODE>(job, s);
+      return launch_gemv_mfl_split<kQ4_K, false, MODE>(job, s);
+    }
+  }
   // bf16 rows of at most 16 chunks: the persistent form (activations resident
   // in registers), one 512-thread workgroup per CU (measured best: 14336 x 4096
   // Q4_K at M = 16 18 us vs 30 us for the one-tile-per-workgroup form)

@@ -294,7 +294,7 @@ __global__ __launch_bounds__(512) void moe_up_mfp_kernel(ExpertPtrs wg, ExpertPt
                                                          const uint16_t* __restrict__ x, int H, int I, int E,
                                                          MoeWs ws) {
   constexpr int W = 8;
-  __shared__ __attribute__((aligned(16))) uint8_t wl[2 * 2 * mfl_unit_lds(W)];
+  __shared__ __attribute__((aligned(16))) uint8_t wl[2 * 2 * mfl_unit_lds<kQ4_K>(W)];
   __shared__ mf_f32x4 part[2][W][2][64];
   __shared__ int tb[kMaxExperts + 1];  // token tiles of the experts before e
   const int lane = threadIdx.x & 63;

@@ -183,6 +183,37 @@ def test_gemv_residual_split_k(qtype, m, xdtype):
     assert np.array_equal(outs[0], outs[1])
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("qtype,n,k,m", [(Q6_K, 4096, 14336, 16), (Q6_K, 4144, 14336, 9),
+                                         (Q4_K, 4144, 12800, 16), (Q4_K, 4096, 14336, 11)])
+def test_gemv_residual_split_k_runs(qtype, n, k, m):
+    """The split launch at the down projection's size: 7 splits x 256-259
+    row tiles dealt to the CUs in equal runs that cross split boundaries
+    (and, at K = 12800 for Q4_K, a last split of two chunks): within the bar
+    of the oracle, the same on every call."""
+    from dracort_amd.kernels import gemv_residual_workspace_bytes, gguf_gemv_residual
+
+    need = gemv_residual_workspace_bytes(qtype, m, n, k)
+    assert need == ((k // 256 + 7) // 8) * m * n * 4
+    blocks, w = quantized(qtype, n, k, 400 + m)
+    q = torch.from_numpy(blocks).cuda()
+    x = activations(m, k, 410 + m, torch.bfloat16).cuda()
+    ref = matmul_ref.linear_ref(x.cpu().float().numpy(), w)
+    r0 = np.random.default_rng(420 + m).standard_normal((m, n), dtype=np.float32)
+    print(f"split-K runs {NAMES[qtype]} [{n},{k}] m={m}", flush=True)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    outs = []
+    for _ in range(2):
+        resid = torch.from_numpy(r0.copy()).cuda()
+        rb = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        gguf_gemv_residual(x, q, qtype, (n, k), resid, rb, workspace=ws)
+        got = resid.cpu().numpy()
+        check_close(got, r0.astype(np.float64) + ref, f"split runs {NAMES[qtype]} [{n},{k}] m={m}")
+        assert np.array_equal(rb.float().cpu().numpy(), _bf16_round(got))
+        outs.append(got)
+    assert np.array_equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("qtype", [Q8_0, Q4_0])
 @pytest.mark.parametrize("xdtype", [torch.float32, torch.bfloat16])
 def test_gemv_single_token_block_formats(qtype, xdtype):

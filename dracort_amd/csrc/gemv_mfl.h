@@ -48,12 +48,18 @@ __host__ __device__ constexpr int mfl_unit_lds(int w) { return 16 * (w * MflChun
 // tile i's summed result.  Q6_K super-blocks sit at even LDS offsets, so
 // each dword field is read as the two aligned dwords around it and realigned
 // (v_alignbyte).
-template <int QT, bool DL, int NR, int W, int U, class TileBase, class Emit>
-__device__ __forceinline__ void mfl_stream_u(const typename MfpTypes<QT>::X (&xr)[16 / W], int chunks, int ntiles,
+// Resident activations of one chunk: bf16 (P = 1), or float32 values as three
+// bf16 planes (P = 3, Q4_K; the chunk math against the codes without bias).
+template <int QT, int P> struct MflX { typedef typename MfpTypes<QT>::X T; };
+template <> struct MflX<kQ4_K, 3> { typedef mf_bf16x8 T[8][3]; };
+
+template <int QT, bool DL, int NR, int W, int U, int P, int NX, class TileBase, class Emit>
+__device__ __forceinline__ void mfl_stream_u(const typename MflX<QT, P>::T (&xr)[NX], int chunks, int ntiles,
                                              int row_bytes, TileBase tile_base, Emit emit, uint8_t* __restrict__ wl,
                                              mf_f32x4 (&part)[2][W][NR][64]) {
-  constexpr int NT = W * 64, CPW = 16 / W;
-  static_assert(U >= 1 && U <= CPW, "units per tile");
+  constexpr int NT = W * 64;
+  static_assert(U >= 1 && U <= NX && NX <= 16 / W, "units per tile");
+  static_assert(P == 1 || (P == 3 && QT == kQ4_K), "three planes: Q4_K");
   static_assert(QT == kQ4_K || (QT == kQ6_K && NR == 1 && (W * 210) % 16 == 0), "Q4_K, or one Q6_K matrix");
   constexpr int CB = MflChunk<QT>::bytes;
   constexpr int UB = W * CB;                     // bytes of one row's span in a unit
@@ -66,10 +72,15 @@ __device__ __forceinline__ void mfl_stream_u(const typename MfpTypes<QT>::X (&xr
   const int q = lane >> 4, nl = lane & 15;
   const int nunits = ntiles * U;
 
-  float sx[CPW][2];  // Q4_K: the resident chunks' group sums
+  float sx[NX][2];  // Q4_K: the resident chunks' group sums
   if constexpr (QT == kQ4_K)
 #pragma unroll
-    for (int j = 0; j < CPW; ++j) mf_group_sums(xr[j], q, sx[j]);
+    for (int j = 0; j < NX; ++j) {
+      if constexpr (P == 1)
+        mf_group_sums(xr[j], q, sx[j]);
+      else
+        mf_group_sums3(xr[j], q, sx[j]);
+    }
 
   // this thread's pieces: row, 16-byte column within the unit's span, LDS destination
   int prow[PPT], pcol[PPT], dst[PPT];
@@ -146,7 +157,10 @@ __device__ __forceinline__ void mfl_stream_u(const typename MfpTypes<QT>::X (&xr
                 wc[r].qs[p][1] = t.y;
               }
             }
-            mf_chunk_q4k_sx<NR>(xr[xj], wc, q, acc, sx[xj]);
+            if constexpr (P == 1)
+              mf_chunk_q4k_sx<NR>(xr[xj], wc, q, acc, sx[xj]);
+            else
+              mf_chunk_q4k_sx3<NR>(xr[xj], wc, q, acc, sx[xj]);
           } else {
             const uint8_t* rp = img + nl * RS;
             const int base = ks * CB;
@@ -207,9 +221,9 @@ __device__ __forceinline__ void mfl_stream(const typename MfpTypes<QT>::X (&xr)[
                                            int row_bytes, TileBase tile_base, Emit emit, uint8_t* __restrict__ wl,
                                            mf_f32x4 (&part)[2][W][NR][64]) {
   if (chunks > W)
-    mfl_stream_u<QT, DL, NR, W, 2>(xr, chunks, ntiles, row_bytes, tile_base, emit, wl, part);
+    mfl_stream_u<QT, DL, NR, W, 2, 1, 16 / W>(xr, chunks, ntiles, row_bytes, tile_base, emit, wl, part);
   else
-    mfl_stream_u<QT, DL, NR, W, 1>(xr, chunks, ntiles, row_bytes, tile_base, emit, wl, part);
+    mfl_stream_u<QT, DL, NR, W, 1, 1, 16 / W>(xr, chunks, ntiles, row_bytes, tile_base, emit, wl, part);
 }
 
 // The Q4_K form (the MoE up projection's stream).
@@ -346,7 +360,7 @@ __global__ __launch_bounds__(W * 64) void gemv_mfl_split_kernel(StreamJob job) {
       for (int v = 0; v < 4; ++v)
         if (4 * q + v < M) pp[(size_t)(4 * q + v) * n] = tot[0][v];
     };
-    mfl_stream_u<QT, DL, 1, W, 1>(xr, nch, nt, row_bytes, tile_base, emit, wl, part);
+    mfl_stream_u<QT, DL, 1, W, 1, 1, 16 / W>(xr, nch, nt, row_bytes, tile_base, emit, wl, part);
     u += nt;
   }
 }

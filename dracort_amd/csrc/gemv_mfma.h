@@ -205,6 +205,33 @@ __device__ __forceinline__ void mf_group_sums(const mf_bf16x8 (&x)[8][1], int q,
   sx[1] = q == 0 ? p[4] : q == 1 ? p[5] : q == 2 ? p[6] : p[7];
 }
 
+// The same for float32 activations held as three bf16 planes (each element's
+// three planes added in float32 first).
+__device__ __forceinline__ void mf_group_sums3(const mf_bf16x8 (&x)[8][3], int q, float (&sx)[2]) {
+  float p[8];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    uint32_t h[3][4];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const uint4 u = __builtin_bit_cast(uint4, x[g][j]);
+      h[j][0] = u.x; h[j][1] = u.y; h[j][2] = u.z; h[j][3] = u.w;
+    }
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = __uint_as_float(h[0][i] << 16) + __uint_as_float(h[1][i] << 16) + __uint_as_float(h[2][i] << 16);
+      const float hi = __uint_as_float(h[0][i] & 0xFFFF0000u) + __uint_as_float(h[1][i] & 0xFFFF0000u) +
+                       __uint_as_float(h[2][i] & 0xFFFF0000u);
+      t += lo + hi;
+    }
+    t += __shfl_xor(t, 16);
+    p[g] = t + __shfl_xor(t, 32);
+  }
+  sx[0] = q == 0 ? p[0] : q == 1 ? p[1] : q == 2 ? p[2] : p[3];
+  sx[1] = q == 0 ? p[4] : q == 1 ? p[5] : q == 2 ? p[6] : p[7];
+}
+
 // acc += the products of one 256-element chunk: activations x (per group, NP
 // bf16 planes) against NR weight rows' codes w; sx (SX): the chunk's group
 // sums from mf_group_sums.
@@ -333,6 +360,50 @@ template <int NR>
 __device__ __forceinline__ void mf_chunk_q4k_sx(const mf_bf16x8 (&x)[8][1], const MfChunk<kQ4_K> (&w)[NR], int q,
                                                 mf_f32x4 (&acc)[NR], const float (&sx)[2]) {
   mf_chunk_q4_impl<kQ4_K, true, NR, true>(x, w, q, acc, sx);
+}
+
+// Q4_K against float32 activations as three bf16 planes, with the chunk's
+// group sums from mf_group_sums3: per group three MFMAs against the exact
+// codes (D = sum x q), t += sc_g D_g, d once per chunk; the min term
+// sum_g m_g S_g from two v_mfma_f32_16x16x4f32 (A = the sums, B = m), times
+// dmin once per chunk.
+template <int NR>
+__device__ __forceinline__ void mf_chunk_q4k_sx3(const mf_bf16x8 (&x)[8][3], const MfChunk<kQ4_K> (&w)[NR], int q,
+                                                 mf_f32x4 (&acc)[NR], const float (&sx)[2]) {
+  const mf_f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  float sc[NR][8], mn[NR][2];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const uint32_t s0 = w[r].head.y, s1 = w[r].head.z, s2 = w[r].head.w;
+    const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, m_lo = s1 & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) sc[r][g] = ubyte_f(g < 4 ? sc_lo : sc_hi, g & 3);
+    mn[r][0] = (float)((m_lo >> (8 * q)) & 0xFFu);
+    mn[r][1] = (float)((m_hi >> (8 * q)) & 0xFFu);
+  }
+  mf_f32x4 t[NR];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const mf_bf16x8 bc = mf_codes_exact<kQ4_K>(w[r], g, q);
+      mf_f32x4 dg = z;
+#pragma unroll
+      for (int j = 2; j >= 0; --j) dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[g][j], bc, dg, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) t[r][v] = g == 0 ? sc[r][g] * dg[v] : fmaf(sc[r][g], dg[v], t[r][v]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const float d = f16_bits_to_f32(w[r].head.x), dmin = f16_bits_to_f32(w[r].head.x >> 16);
+    mf_f32x4 t2 = __builtin_amdgcn_mfma_f32_16x16x4f32(sx[0], mn[r][0], z, 0, 0, 0);
+    t2 = __builtin_amdgcn_mfma_f32_16x16x4f32(sx[1], mn[r][1], t2, 0, 0, 0);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[r][v] = fmaf(-dmin, t2[v], fmaf(d, t[r][v], acc[r][v]));
+  }
 }
 
 // The three bf16 planes of a float32 value (hi, mid, lo: each the

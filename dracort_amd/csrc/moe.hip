@@ -50,9 +50,14 @@ struct MoeWs {
   uint16_t* hp;     // [3][T*k, inter] the same as three bf16 planes (matrix-core path)
   size_t hp_plane;  // elements per plane: T*k*inter
   float* yk;        // [T*k, hidden] expert outputs
+  float* yks;       // [splits][T*k, hidden] the matrix-core down projection's split sums
+  int tk;           // T*k
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+// K splits of the LDS-staged down projection (eight 256-element chunks each).
+static int moe_down_splits(int64_t I) { return (int)((I / 256 + 7) / 8); }
 
 static size_t moe_ws_layout(int64_t T, int64_t H, int64_t I, int E, int k, char* base, MoeWs* ws) {
   const size_t tk = (size_t)T * k;
@@ -73,6 +78,8 @@ static size_t moe_ws_layout(int64_t T, int64_t H, int64_t I, int E, int k, char*
   w.hp = (uint16_t*)take(3 * tk * (size_t)I * 2);
   w.hp_plane = tk * (size_t)I;
   w.yk = (float*)take(tk * (size_t)H * 4);
+  w.yks = (float*)take((size_t)moe_down_splits(I) * tk * (size_t)H * 4);
+  w.tk = (int)tk;
   if (ws) *ws = w;
   return off;
 }
@@ -414,6 +421,94 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertPtrs wd, int H
   }
 }
 
+// The down projection split along K, on the small-batch GEMV's LDS stream:
+// units (token tile of an expert, split of eight chunks, 16-row tile of
+// W_down[e]) in that order, one workgroup per CU taking an equal run.  For
+// each (token tile, split) of its run a workgroup holds that split's h planes
+// (16 assignment rows x 8 chunks x 3 bf16 planes, one chunk per wave) in
+// registers and streams the row tiles through LDS (mfl_stream_u, three-plane
+// chunk math against exact codes); each tile's raw sums go to yks[split], and
+// moe_combine_split_kernel adds the splits in order.  Q4_K, H and I multiples
+// of 256.
+__global__ __launch_bounds__(512) void moe_down_mfl_kernel(ExpertPtrs wd, int H, int I, int E, MoeWs ws) {
+  constexpr int W = 8;
+  __shared__ __attribute__((aligned(16))) uint8_t wl[2 * mfl_unit_lds<kQ4_K>(W)];
+  __shared__ mf_f32x4 part[2][W][1][64];
+  __shared__ int tb[kMaxExperts + 1];  // token tiles of the experts before e
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, nl = lane & 15;
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int e = 0; e < E; ++e) {
+      tb[e] = acc;
+      acc += (ws.counts[e] + 15) >> 4;
+    }
+    tb[E] = acc;
+  }
+  __syncthreads();
+  const int chunks = I >> 8, splits = (chunks + W - 1) / W, rt = H >> 4;
+  const int per = splits * rt;  // units per token tile
+  const int units = tb[E] * per;
+  const int G = gridDim.x, b = blockIdx.x;
+  const int u1 = (int)((int64_t)units * (b + 1) / G);
+  const int row_bytes = chunks * 144;
+  const uint32_t mat_bytes = (uint32_t)H * (uint32_t)row_bytes;
+  const size_t tk = (size_t)ws.tk;  // assignment rows
+  for (int u = (int)((int64_t)units * b / G); u < u1;) {
+    const int item = u / per, rem = u - item * per;
+    const int s = rem / rt, r0 = rem - s * rt;
+    const int nt = min(u1 - u, rt - r0);
+    int e = 0;
+    while (tb[e + 1] <= item) ++e;  // item < tb[E]; experts without tokens are skipped
+    e = __builtin_amdgcn_readfirstlane(e);
+    const int t0 = 16 * (item - tb[e]);
+    const int off = ws.offsets[e];
+    const int mt = min(16, ws.counts[e] - t0);
+    const int c0 = W * s, nch = min(W, chunks - c0);
+    mf_bf16x8 xr[1][8][3];
+    {
+      const uint16_t* xrow = ws.hp + (size_t)(off + t0 + min(nl, mt - 1)) * I;
+      const int cc = min(c0 + ks, chunks - 1);
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        const uint16_t* xp = xrow + cc * 256 + mf_pos<kQ4_K>(g, q);
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+          xr[0][g][j] = __builtin_bit_cast(mf_bf16x8, *reinterpret_cast<const uint4*>(xp + j * ws.hp_plane));
+      }
+    }
+    const uint8_t* const wp = wd.p[e];
+    auto tile_base = [=](int i, int) {
+      return MfRow{make_rsrc(wp, mat_bytes), (r0 + i) * 16 * row_bytes + c0 * 144};
+    };
+    float* const out = ws.yks + ((size_t)s * tk + off + t0) * H + nl;
+    auto emit = [=](int i, const mf_f32x4 (&tot)[1]) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (4 * q + v < mt) out[(size_t)(4 * q + v) * H + 16 * (r0 + i)] = tot[0][v];
+    };
+    mfl_stream_u<kQ4_K, false, 1, W, 1, 3, 1>(xr, nch, nt, row_bytes, tile_base, emit, wl, part);
+    u += nt;
+  }
+}
+
+// y[t] = sum over the token's k slots, in order, of w * (the slot's split sums added in split order).
+__global__ __launch_bounds__(256) void moe_combine_split_kernel(float* __restrict__ y, int H, int k, int splits,
+                                                                MoeWs ws) {
+  const int t = blockIdx.y;
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= H) return;
+  float acc = 0.f;
+  for (int j = 0; j < k; ++j) {
+    const int p = ws.slot_pos[t * k + j];
+    float v = ws.yks[(size_t)p * H + n];
+    for (int s = 1; s < splits; ++s) v += ws.yks[((size_t)s * ws.tk + p) * H + n];
+    acc = acc + v * ws.sel_w[t * k + j];
+  }
+  y[(size_t)t * H + n] = acc;
+}
+
 __global__ __launch_bounds__(256) void moe_combine_kernel(float* __restrict__ y, int H, int k, MoeWs ws) {
   const int t = blockIdx.y;
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
@@ -455,6 +550,14 @@ static int launch_moe(const ExpertPtrs& wg, const ExpertPtrs& wu, const ExpertPt
         hipLaunchKernelGGL((moe_up_mfma_kernel<QT, false>), dim3((unsigned)(I / 16), (unsigned)E, zt), dim3(256), 0, s,
                            wg, wu, x, H, I, ws);
       if (int rc = check_launch("moe_up_mfma")) return rc;
+      if constexpr (QT == kQ4_K) {
+        // down split along K over one workgroup per CU, then the ordered split sums in the combine
+        hipLaunchKernelGGL(moe_down_mfl_kernel, dim3((unsigned)device_cus()), dim3(512), 0, s, wd, H, I, E, ws);
+        if (int rc = check_launch("moe_down_mfl")) return rc;
+        hipLaunchKernelGGL(moe_combine_split_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, s,
+                           y, H, k, moe_down_splits(I), ws);
+        return check_launch("moe_combine");
+      }
       hipLaunchKernelGGL((moe_down_mfma_kernel<QT, 4>), dim3((unsigned)(H / 64), (unsigned)E, zt), dim3(256), 0, s, wd,
                          H, I, ws);
       if (int rc = check_launch("moe_down_mfma")) return rc;

@@ -84,45 +84,109 @@ static size_t moe_ws_layout(int64_t T, int64_t H, int64_t I, int E, int k, char*
   return off;
 }
 
+// Top-k of one token's logits (ties: the lower expert id), softmax over the
+// k, renormalised, slots sorted by expert id.
+__device__ __forceinline__ void moe_topk(const float* __restrict__ lg, int E, int k, int (&idx)[kMaxTopK],
+                                         float (&ex)[kMaxTopK]) {
+  float val[kMaxTopK];
+  uint64_t taken = 0;
+  for (int j = 0; j < k; ++j) {
+    int best = -1;
+    float bv = 0.f;
+    for (int e = 0; e < E; ++e) {
+      if (taken >> e & 1ull) continue;
+      const float v = lg[e];
+      if (best < 0 || v > bv) { best = e; bv = v; }
+    }
+    taken |= 1ull << best;
+    idx[j] = best;
+    val[j] = bv;
+  }
+  float s = 0.f;
+  for (int j = 0; j < k; ++j) { ex[j] = __expf(val[j] - val[0]); s += ex[j]; }
+  float s2 = 0.f;
+  for (int j = 0; j < k; ++j) { ex[j] = ex[j] / s; s2 += ex[j]; }
+  for (int j = 0; j < k; ++j) ex[j] = ex[j] / s2;
+  for (int a = 1; a < k; ++a) {  // insertion sort by expert id
+    int ie = idx[a];
+    float we = ex[a];
+    int b = a - 1;
+    while (b >= 0 && idx[b] > ie) { idx[b + 1] = idx[b]; ex[b + 1] = ex[b]; --b; }
+    idx[b + 1] = ie;
+    ex[b + 1] = we;
+  }
+}
+
 __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int T, int E, int k,
                                                         MoeWs ws) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int offs[kMaxExperts + 1];
   __shared__ int running[kMaxExperts];
   __shared__ int wave_tot[4];
+  __shared__ int wcnt[4][kMaxExperts];  // single-pass grouping: slots of expert e per wave
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  if (T <= 256) {
+    // one token per thread, its slots in registers: the same routing and the
+    // same grouping (tokens of expert e in ascending token order) as the
+    // general path below, with one ballot per expert and wave instead of a
+    // pass with barriers per expert
+    const int t = tid;
+    int idx[kMaxTopK];
+    float ex[kMaxTopK];
+    if (t < T) {
+      moe_topk(logits + (size_t)t * E, E, k, idx, ex);
+      for (int j = 0; j < k; ++j) {
+        ws.sel_e[t * k + j] = idx[j];
+        ws.sel_w[t * k + j] = ex[j];
+      }
+    }
+    int rk[kMaxTopK] = {};
+    for (int e = 0; e < E; ++e) {
+      bool has = false;
+#pragma unroll
+      for (int j = 0; j < kMaxTopK; ++j) has |= t < T && j < k && idx[j] == e;
+      const uint64_t mask = __ballot(has);
+      const int r = __popcll(mask & ((1ull << lane) - 1ull));
+#pragma unroll
+      for (int j = 0; j < kMaxTopK; ++j)
+        if (t < T && j < k && idx[j] == e) rk[j] = r;
+      if (lane == 0) wcnt[wave][e] = __popcll(mask);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int acc = 0;
+      for (int e = 0; e < E; ++e) {
+        offs[e] = acc;
+        acc += wcnt[0][e] + wcnt[1][e] + wcnt[2][e] + wcnt[3][e];
+      }
+      offs[E] = acc;
+    }
+    __syncthreads();
+    if (tid < E) {
+      ws.counts[tid] = offs[tid + 1] - offs[tid];
+      ws.offsets[tid] = offs[tid];
+    }
+    if (tid == 0) ws.offsets[E] = offs[E];
+    if (t < T)
+#pragma unroll
+      for (int j = 0; j < kMaxTopK; ++j) {
+        if (j >= k) break;
+        const int e = idx[j];
+        int before = 0;
+        for (int w = 0; w < wave; ++w) before += wcnt[w][e];
+        const int pos = offs[e] + before + rk[j];
+        ws.assign_tok[pos] = t;
+        ws.slot_pos[t * k + j] = pos;
+      }
+    return;
+  }
 
   // 1. top-k, softmax, renormalise, sort slots by expert
   for (int t = tid; t < T; t += 256) {
-    const float* lg = logits + (size_t)t * E;
     int idx[kMaxTopK];
-    float val[kMaxTopK];
-    uint64_t taken = 0;
-    for (int j = 0; j < k; ++j) {
-      int best = -1;
-      float bv = 0.f;
-      for (int e = 0; e < E; ++e) {
-        if (taken >> e & 1ull) continue;
-        const float v = lg[e];
-        if (best < 0 || v > bv) { best = e; bv = v; }
-      }
-      taken |= 1ull << best;
-      idx[j] = best;
-      val[j] = bv;
-    }
-    float ex[kMaxTopK], s = 0.f;
-    for (int j = 0; j < k; ++j) { ex[j] = __expf(val[j] - val[0]); s += ex[j]; }
-    float s2 = 0.f;
-    for (int j = 0; j < k; ++j) { ex[j] = ex[j] / s; s2 += ex[j]; }
-    for (int j = 0; j < k; ++j) ex[j] = ex[j] / s2;
-    for (int a = 1; a < k; ++a) {  // insertion sort by expert id
-      int ie = idx[a];
-      float we = ex[a];
-      int b = a - 1;
-      while (b >= 0 && idx[b] > ie) { idx[b + 1] = idx[b]; ex[b + 1] = ex[b]; --b; }
-      idx[b + 1] = ie;
-      ex[b + 1] = we;
-    }
+    float ex[kMaxTopK];
+    moe_topk(logits + (size_t)t * E, E, k, idx, ex);
     for (int j = 0; j < k; ++j) {
       ws.sel_e[t * k + j] = idx[j];
       ws.sel_w[t * k + j] = ex[j];

@@ -60,6 +60,18 @@ def test_moe_edge_routing():
     check_close(y, ref, "moe top1 f32")
 
 
+def test_moe_route_paths():
+    """Up to 256 tokens are routed one per thread (one ballot per expert and
+    wave), more by the general grouping loop; both against the oracle, with
+    ties in the logits (rounded to 0.5: equal logits go to the lower expert),
+    up to 64 experts and top-8."""
+    for t, e, k in ((256, 16, 4), (300, 8, 2), (130, 64, 8)):
+        logits = (np.round(np.random.default_rng(40 + t).standard_normal((t, e)) * 2) / 2).astype(np.float32)
+        print(f"moe routing T={t} E={e} k={k}", flush=True)
+        y, ref = _run(Q4_K, t, 256, 512, e, k, seed=41 + e, logits=logits)
+        check_close(y, ref, f"moe routing T={t} E={e} k={k}")
+
+
 @pytest.mark.parametrize("qtype", [Q4_K, Q4_0])
 def test_moe_matrix_core_f32(qtype):
     """float32 hidden states on the matrix-core experts (three bf16 planes),

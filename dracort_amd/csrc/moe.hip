@@ -85,7 +85,9 @@ static size_t moe_ws_layout(int64_t T, int64_t H, int64_t I, int E, int k, char*
 }
 
 // Top-k of one token's logits (ties: the lower expert id), softmax over the
-// k, renormalised, slots sorted by expert id.
+// k, renormalised, slots sorted by expert id.  EM > 0: at most EM experts, the
+// expert loop unrolled (lg may then be a register array).
+template <int EM = 0>
 __device__ __forceinline__ void moe_topk(const float* __restrict__ lg, int E, int k, int (&idx)[kMaxTopK],
                                          float (&ex)[kMaxTopK]) {
   float val[kMaxTopK];
@@ -93,7 +95,9 @@ __device__ __forceinline__ void moe_topk(const float* __restrict__ lg, int E, in
   for (int j = 0; j < k; ++j) {
     int best = -1;
     float bv = 0.f;
-    for (int e = 0; e < E; ++e) {
+#pragma unroll
+    for (int e = 0; e < (EM > 0 ? EM : E); ++e) {
+      if (EM > 0 && e >= E) break;
       if (taken >> e & 1ull) continue;
       const float v = lg[e];
       if (best < 0 || v > bv) { best = e; bv = v; }
@@ -135,7 +139,15 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
     int idx[kMaxTopK];
     float ex[kMaxTopK];
     if (t < T) {
-      moe_topk(logits + (size_t)t * E, E, k, idx, ex);
+      if (E <= 16) {
+        float lr[16];  // the token's logits, loaded once (unrolled: static register indices)
+        const float* lg = logits + (size_t)t * E;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) lr[e] = e < E ? lg[e] : 0.f;
+        moe_topk<16>(lr, E, k, idx, ex);
+      } else {
+        moe_topk(logits + (size_t)t * E, E, k, idx, ex);
+      }
       for (int j = 0; j < k; ++j) {
         ws.sel_e[t * k + j] = idx[j];
         ws.sel_w[t * k + j] = ex[j];
@@ -557,20 +569,25 @@ __global__ __launch_bounds__(512) void moe_down_mfl_kernel(ExpertPtrs wd, int H,
   }
 }
 
-// y[t] = sum over the token's k slots, in order, of w * (the slot's split sums added in split order).
+// y[t] = sum over the token's k slots, in order, of w * (the slot's split sums
+// added in split order); four consecutive outputs per thread (H a multiple of 4).
 __global__ __launch_bounds__(256) void moe_combine_split_kernel(float* __restrict__ y, int H, int k, int splits,
                                                                 MoeWs ws) {
   const int t = blockIdx.y;
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int n = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
   if (n >= H) return;
-  float acc = 0.f;
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < k; ++j) {
     const int p = ws.slot_pos[t * k + j];
-    float v = ws.yks[(size_t)p * H + n];
-    for (int s = 1; s < splits; ++s) v += ws.yks[((size_t)s * ws.tk + p) * H + n];
-    acc = acc + v * ws.sel_w[t * k + j];
+    const float w = ws.sel_w[t * k + j];
+    float4 v = *reinterpret_cast<const float4*>(ws.yks + (size_t)p * H + n);
+    for (int s = 1; s < splits; ++s) {
+      const float4 u = *reinterpret_cast<const float4*>(ws.yks + ((size_t)s * ws.tk + p) * H + n);
+      v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+    }
+    acc.x = acc.x + v.x * w; acc.y = acc.y + v.y * w; acc.z = acc.z + v.z * w; acc.w = acc.w + v.w * w;
   }
-  y[(size_t)t * H + n] = acc;
+  *reinterpret_cast<float4*>(y + (size_t)t * H + n) = acc;
 }
 
 __global__ __launch_bounds__(256) void moe_combine_kernel(float* __restrict__ y, int H, int k, MoeWs ws) {
@@ -618,8 +635,8 @@ static int launch_moe(const ExpertPtrs& wg, const ExpertPtrs& wu, const ExpertPt
         // down split along K over one workgroup per CU, then the ordered split sums in the combine
         hipLaunchKernelGGL(moe_down_mfl_kernel, dim3((unsigned)device_cus()), dim3(512), 0, s, wd, H, I, E, ws);
         if (int rc = check_launch("moe_down_mfl")) return rc;
-        hipLaunchKernelGGL(moe_combine_split_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, s,
-                           y, H, k, moe_down_splits(I), ws);
+        hipLaunchKernelGGL(moe_combine_split_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T), dim3(256), 0,
+                           s, y, H, k, moe_down_splits(I), ws);
         return check_launch("moe_combine");
       }
       hipLaunchKernelGGL((moe_down_mfma_kernel<QT, 4>), dim3((unsigned)(H / 64), (unsigned)E, zt), dim3(256), 0, s, wd,

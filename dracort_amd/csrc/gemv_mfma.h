@@ -93,6 +93,21 @@ __device__ __forceinline__ mf_bf16x8 mf_codes(const MfChunk<QT>& c, int g, int q
   return __builtin_bit_cast(mf_bf16x8, v);
 }
 
+// Byte I of w as float (v_cvt_f32_ubyteI).
+template <int I>
+__device__ __forceinline__ float cvt_ubyte(uint32_t w) {
+  float f;
+  if constexpr (I == 0)
+    asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(w));
+  else if constexpr (I == 1)
+    asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(w));
+  else if constexpr (I == 2)
+    asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(w));
+  else
+    asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(w));
+  return f;
+}
+
 // B operand without the 128 bias: the codes themselves as bf16 (exact small
 // integers; byte -> float -> upper half of the float bits), used with float32
 // activations, whose three-plane products otherwise lose too many bits in the
@@ -108,12 +123,18 @@ __device__ __forceinline__ mf_bf16x8 mf_codes_exact(const MfChunk<QT>& c, int g,
     w0 = hi ? nib_hi(c.qs[g][0]) : nib_lo(c.qs[g][0]);
     w1 = hi ? nib_hi(c.qs[g][1]) : nib_lo(c.qs[g][1]);
   }
+  // each code to float (exact; one v_cvt_f32_ubyteN per code of the masked
+  // word -- left to itself the compiler extracts every byte first), pairs to
+  // bf16 (exact: integers < 256) with one v_cvt_pk_bf16_f32 per pair
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
   uint32_t v[4];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const uint32_t w = i == 0 ? w0 : w1;
-    v[2 * i] = (__float_as_uint(ubyte_f(w, 0)) >> 16) | (__float_as_uint(ubyte_f(w, 1)) & 0xFFFF0000u);
-    v[2 * i + 1] = (__float_as_uint(ubyte_f(w, 2)) >> 16) | (__float_as_uint(ubyte_f(w, 3)) & 0xFFFF0000u);
+    const f32x2 lo = {cvt_ubyte<0>(w), cvt_ubyte<1>(w)}, hi = {cvt_ubyte<2>(w), cvt_ubyte<3>(w)};
+    v[2 * i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2v));
+    v[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2v));
   }
   return __builtin_bit_cast(mf_bf16x8, v);
 }

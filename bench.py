@@ -324,8 +324,9 @@ def suite(reps: int, gemv_only: bool = False):
     wg = [synthetic_weight(inter, hid, 12, gen, "cuda").data for _ in range(ne)]
     wu = [synthetic_weight(inter, hid, 12, gen, "cuda").data for _ in range(ne)]
     wd = [synthetic_weight(hid, inter, 12, gen, "cuda").data for _ in range(ne)]
-    x = torch.randn((tok, hid), device="cuda").to(torch.bfloat16)
-    logits = torch.randn((tok, ne), device="cuda")
+    # seeded like the weights: the routing (and so the number of 16-token tiles) is the same every run
+    x = torch.randn((tok, hid), generator=gen, device="cuda").to(torch.bfloat16)
+    logits = torch.randn((tok, ne), generator=gen, device="cuda")
     ws = torch.empty(moe_workspace_bytes(tok, hid, inter, ne, 2), dtype=torch.uint8, device="cuda")
     y = torch.empty((tok, hid), device="cuda")
     ms = time_launches([lambda: gguf_moe(x, logits, wg, wu, wd, 12, inter, top_k=2, workspace=ws, out=y)], reps)
@@ -419,8 +420,9 @@ def moe_probe(reps: int):
     wg = [synthetic_weight(inter, hid, 12, gen, "cuda").data for _ in range(ne)]
     wu = [synthetic_weight(inter, hid, 12, gen, "cuda").data for _ in range(ne)]
     wd = [synthetic_weight(hid, inter, 12, gen, "cuda").data for _ in range(ne)]
-    x = torch.randn((tok, hid), device="cuda").to(torch.bfloat16)
-    logits = torch.randn((tok, ne), device="cuda")
+    # seeded like the weights: the routing (and so the number of 16-token tiles) is the same every run
+    x = torch.randn((tok, hid), generator=gen, device="cuda").to(torch.bfloat16)
+    logits = torch.randn((tok, ne), generator=gen, device="cuda")
     ws = torch.empty(moe_workspace_bytes(tok, hid, inter, ne, 2), dtype=torch.uint8, device="cuda")
     y = torch.empty((tok, hid), device="cuda")
     for _ in range(reps):
@@ -695,8 +697,9 @@ def config_suite(reps: int, cpu: bool = True):
     wg = [synthetic_weight(inter, hid, 12, gen, "cuda").data for _ in range(ne)]
     wu = [synthetic_weight(inter, hid, 12, gen, "cuda").data for _ in range(ne)]
     wd = [synthetic_weight(hid, inter, 12, gen, "cuda").data for _ in range(ne)]
-    x = torch.randn((tok, hid), device="cuda").to(torch.bfloat16)
-    logits = torch.randn((tok, ne), device="cuda")
+    # seeded like the weights: the routing (and so the number of 16-token tiles) is the same every run
+    x = torch.randn((tok, hid), generator=gen, device="cuda").to(torch.bfloat16)
+    logits = torch.randn((tok, ne), generator=gen, device="cuda")
     ws = torch.empty(moe_workspace_bytes(tok, hid, inter, ne, 2), dtype=torch.uint8, device="cuda")
     y = torch.empty((tok, hid), device="cuda")
     ms = time_launches([lambda: gguf_moe(x, logits, wg, wu, wd, 12, inter, top_k=2, workspace=ws, out=y)], reps)

@@ -72,16 +72,6 @@ __device__ __forceinline__ void mfl_stream_u(const typename MflX<QT, P>::T (&xr)
   const int q = lane >> 4, nl = lane & 15;
   const int nunits = ntiles * U;
 
-  float sx[NX][2];  // Q4_K: the resident chunks' group sums
-  if constexpr (QT == kQ4_K)
-#pragma unroll
-    for (int j = 0; j < NX; ++j) {
-      if constexpr (P == 1)
-        mf_group_sums(xr[j], q, sx[j]);
-      else
-        mf_group_sums3(xr[j], q, sx[j]);
-    }
-
   // this thread's pieces: row, 16-byte column within the unit's span, LDS destination
   int prow[PPT], pcol[PPT], dst[PPT];
 #pragma unroll
@@ -122,6 +112,17 @@ __device__ __forceinline__ void mfl_stream_u(const typename MflX<QT, P>::T (&xr)
   if (ntiles <= 0) return;
   issue(0, stg[0]);
   issue(1, stg[1]);
+  // the resident chunks' group sums (Q4_K) once the first weight requests are
+  // out: waiting for the activations then overlaps the weights' latency
+  float sx[NX][2];
+  if constexpr (QT == kQ4_K)
+#pragma unroll
+    for (int j = 0; j < NX; ++j) {
+      if constexpr (P == 1)
+        mf_group_sums(xr[j], q, sx[j]);
+      else
+        mf_group_sums3(xr[j], q, sx[j]);
+    }
   commit(stg[0], wl);
   issue(2, stg[0]);
   __syncthreads();
